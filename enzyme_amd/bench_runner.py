@@ -1,0 +1,826 @@
+"""Compile + device-bench pipeline for HIP variant modules, and its durable
+result store.
+
+Structure and contracts follow src/axon/bench_runner.py of the reference:
+
+* `run_hip_bench` (the reference's `run_nki_bench`, :576-825) draws the
+  seeded inputs, expands `tile_options ** len(tile_args)`, applies the
+  module's tile manifest and the budgeted selection, resumes from
+  `results.csv`, and streams every remaining key through a compile worker
+  and a device worker, appending exactly one terminal row per key.
+* `_stream_compile_bench` (:491-559) keeps at most `AXON_MAX_LIVE_NEFFS`
+  keys between compile and terminal row; a compile and a bench overlap.
+* The store (`result_columns`, `read_result_keys`, `_append_result_row`,
+  `publish_results`, :364-479) is byte-compatible: same columns, one record
+  per physical line, torn tails truncated, publication only on exact key
+  coverage.
+
+What the workers do is this backend's own:
+
+* compile worker `_compile_one_variant` resolves one TILES_IN_BLOCK_* tuple
+  against libaxon_hip.so's ahead-of-time instantiation table
+  (`axon_variant_check`). An illegal tuple is the reference's "assert"
+  outcome. A legal one writes a launch plan (`kernel.plan.json`) into the
+  key's artefact directory; truth is on disk, as in the reference. It never
+  initialises the HIP runtime.
+* device worker `_bench_one_artifact` runs in a spawned process pinned to
+  one GPU through `HIP_VISIBLE_DEVICES` (set before torch is imported),
+  copies the inputs to HBM, and times each launch with a pair of HIP events
+  on the launch stream. To keep the 256 MB Infinity Cache from serving
+  inputs, launches rotate over enough copies of the input/output set to
+  exceed `AXON_ROTATE_BYTES` (default 1 GiB).
+"""
+
+from __future__ import annotations
+
+import csv
+import importlib.util
+import io
+import json
+import math
+import multiprocessing
+import os
+import shutil
+import sys
+import time
+from collections import Counter, deque
+from collections.abc import Iterator, Sequence
+from concurrent.futures import FIRST_COMPLETED, Executor, ProcessPoolExecutor, wait
+from dataclasses import asdict, dataclass
+from itertools import product
+from pathlib import Path
+from statistics import median
+from typing import Any
+
+import numpy as np
+
+from enzyme_amd import dtypes as _dt
+from enzyme_amd.candidate_filter import read_manifest, rejection_reason, select_diverse
+from enzyme_amd.kernel_spec import SEED, KernelSpec
+from enzyme_amd.paths import RunPaths
+
+__all__ = [
+    "run_hip_bench",
+    "run_nki_bench",
+    "run_baseline",
+    "BenchStats",
+    "BenchError",
+    "clear_stale_artifacts",
+    "publish_results",
+]
+
+DEFAULT_TARGET = "gfx950"
+ROTATE_BYTES_DEFAULT = 1 << 30
+MAX_ROTATE_SETS = 64
+HIP_META_NAME = "__axon_hip_kernel__"
+
+
+@dataclass(frozen=True)
+class BenchStats:
+    mean_ms: float | None
+    median_ms: float | None
+    min_ms: float | None
+    max_ms: float | None
+    std_dev_ms: float | None
+    outputs: tuple[np.ndarray, ...] | None = None
+
+    @classmethod
+    def from_durations(
+        cls, durations_ms: Sequence[float], outputs: tuple[np.ndarray, ...] | None = None
+    ) -> "BenchStats":
+        if not durations_ms:
+            return cls(None, None, None, None, None, outputs)
+        d = [float(x) for x in durations_ms]
+        mean = sum(d) / len(d)
+        std = math.sqrt(sum((x - mean) ** 2 for x in d) / len(d))
+        return cls(mean, median(d), min(d), max(d), std, outputs)
+
+
+@dataclass(frozen=True)
+class BenchError:
+    message: str
+
+    @classmethod
+    def from_exception(cls, e: BaseException) -> "BenchError":
+        return cls(message=f"{type(e).__name__}: {e}")
+
+
+BenchResult = BenchStats | BenchError
+
+
+# ---------------------------------------------------------------------------
+# variant modules
+# ---------------------------------------------------------------------------
+def _load_kernel_from_path(kernel_path: str, kernel_attr: str):
+    """Import a variant module by absolute path under a per-path module name
+    (so different (v, t) modules never collide in one process)."""
+    key = "_axon_variant_" + kernel_path.replace("/", "_").replace("\\", "_")
+    mod = sys.modules.get(key)
+    if mod is None:
+        spec = importlib.util.spec_from_file_location(key, kernel_path)
+        if spec is None or spec.loader is None:
+            raise ImportError(f"could not load variant module from {kernel_path}")
+        mod = importlib.util.module_from_spec(spec)
+        sys.modules[key] = mod
+        spec.loader.exec_module(mod)
+    return getattr(mod, kernel_attr)
+
+
+def read_hip_meta(module_path: str | Path) -> dict[str, Any] | None:
+    """The literal `__axon_hip_kernel__` record of a variant module, read with
+    `ast` (no import); None when absent or not a literal."""
+    import ast
+
+    path = Path(module_path)
+    if not path.is_file():
+        return None
+    try:
+        tree = ast.parse(path.read_text(), filename=str(path))
+        for stmt in tree.body:
+            if isinstance(stmt, ast.Assign) and any(
+                isinstance(t, ast.Name) and t.id == HIP_META_NAME for t in stmt.targets
+            ):
+                value = ast.literal_eval(stmt.value)
+                return value if isinstance(value, dict) else None
+    except (OSError, SyntaxError, ValueError):
+        return None
+    return None
+
+
+# ---------------------------------------------------------------------------
+# workers
+# ---------------------------------------------------------------------------
+def _init_visible_devices(device_spec) -> None:
+    """Device-pool initializer: pin the worker to one GPU before torch loads."""
+    os.environ["HIP_VISIBLE_DEVICES"] = str(device_spec)
+
+
+def _init_compile_worker() -> None:
+    """Compile workers never run kernels; a blank device pin is dropped so no
+    library underneath misreads it."""
+    raw = os.environ.get("HIP_VISIBLE_DEVICES")
+    if raw is not None and not raw.strip():
+        os.environ.pop("HIP_VISIBLE_DEVICES", None)
+
+
+def _compile_one_variant(args):
+    """(module, attr, tile_values, call_args, tile_kwargs, artifact, target, lnc)
+    -> (tile_values, artifact | None, error | None).
+
+    `call_args` is `(dims, dtype_codes)`. The artefact directory is emptied
+    first, so a plan on disk afterwards can only be this call's product."""
+    module_path, kernel_attr, key, call_args, call_kwargs, artifact_path, target, lnc = args
+    del kernel_attr, lnc
+    art_dir = os.path.dirname(artifact_path)
+    if os.path.isdir(art_dir):
+        shutil.rmtree(art_dir)
+    os.makedirs(art_dir, exist_ok=True)
+    meta = read_hip_meta(module_path)
+    if meta is None:
+        return (key, None, f"{module_path} has no {HIP_META_NAME} record")
+    if target and target != meta.get("target", DEFAULT_TARGET):
+        return (key, None, f"module built for {meta.get('target')}, asked for {target}")
+    from enzyme_amd import hip
+
+    dims, dtype_codes = call_args
+    tile_args = tuple(meta["tile_args"])
+    tiles = tuple(int(call_kwargs[a]) for a in tile_args)
+    try:
+        status, why = hip.check(meta["kernel"], int(meta["hw_variant"]), tiles, dims, dtype_codes)
+        if status == hip.AXON_EINVAL:
+            return (key, None, "assert")
+        if status != hip.AXON_OK:
+            return (key, None, why or f"status {status}")
+        plan = {
+            "kernel": meta["kernel"],
+            "hw_variant": int(meta["hw_variant"]),
+            "tile_variant": int(meta.get("tile_variant", 0)),
+            "tile_args": list(tile_args),
+            "tiles": list(tiles),
+            "dims": [int(d) for d in dims],
+            "dtypes": [int(c) for c in dtype_codes],
+            "target": target or DEFAULT_TARGET,
+            "workspace_bytes": hip.workspace_bytes(
+                meta["kernel"], int(meta["hw_variant"]), tiles, dims, dtype_codes
+            ),
+            "library": str(hip.LIB_PATH),
+            "library_mtime": os.path.getmtime(hip.LIB_PATH),
+        }
+    except Exception as e:  # a broken library or module is this key's failure
+        return (key, None, f"{type(e).__name__}: {e}")
+    tmp = artifact_path + ".tmp"
+    with open(tmp, "w") as f:
+        json.dump(plan, f, indent=1)
+    os.replace(tmp, artifact_path)
+    if os.path.getsize(artifact_path) > 0:
+        return (key, artifact_path, None)
+    return (key, None, "artifact_missing")
+
+
+def _bench_one_artifact(args) -> BenchStats:
+    """(module, attr, tile_values, tile_args, inputs, artifact, warmup, bench)
+    -> BenchStats with per-launch HIP-event durations and the outputs of one
+    launch on the first buffer set (as fp32 numpy arrays)."""
+    (module_path, kernel_attr, tile_values, tile_args, inputs, artifact_path, warmup, bench) = args
+    import inspect
+
+    import torch
+
+    from enzyme_amd import hip
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("no GPU visible to the device worker")
+    entry = _load_kernel_from_path(module_path, kernel_attr)
+    params = [p for p in inspect.signature(entry).parameters if p not in set(tile_args)]
+    if len(params) != len(inputs):
+        raise ValueError(
+            f"bench: kernel has {len(params)} data params {params} but got {len(inputs)} input arrays"
+        )
+    with open(artifact_path) as f:
+        plan = json.load(f)
+    dev = torch.device("cuda", 0)
+    host = [_dt.to_torch(a) for a in inputs]
+    set0 = [t.to(dev) for t in host]
+    ln = hip.Launcher(plan["kernel"], plan["hw_variant"], plan["tiles"], plan["dims"], set0)
+    per_set = sum(t.numel() * t.element_size() for t in set0) + sum(
+        t.numel() * t.element_size() for t in ln.outputs
+    )
+    rotate = int(os.environ.get("AXON_ROTATE_BYTES") or ROTATE_BYTES_DEFAULT)
+    n_sets = 1 if per_set == 0 else min(MAX_ROTATE_SETS, max(1, math.ceil(rotate / per_set)))
+    free, _ = torch.cuda.mem_get_info(dev)
+    n_sets = max(1, min(n_sets, int(0.5 * free // max(per_set, 1))))
+    sets = [(set0, ln.outputs)]
+    for _ in range(n_sets - 1):
+        sets.append(([t.clone() for t in set0], [torch.empty_like(o) for o in ln.outputs]))
+
+    stream = torch.cuda.current_stream(dev)
+    for i in range(max(0, int(warmup))):
+        ln.rebind(*sets[i % n_sets])
+        ln.launch(stream)
+    torch.cuda.synchronize(dev)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(bench)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(bench)]
+    for i in range(bench):
+        ln.rebind(*sets[(i + 1) % n_sets])
+        starts[i].record(stream)
+        ln.launch(stream)
+        ends[i].record(stream)
+    torch.cuda.synchronize(dev)
+    durations = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    # Outputs of a fresh launch on the first set: zero it first, so a
+    # variant that leaves part of the output unwritten cannot pass on stale
+    # values from the timing loop.
+    for o in sets[0][1]:
+        o.zero_()
+    ln.rebind(*sets[0])
+    ln.launch(stream)
+    torch.cuda.synchronize(dev)
+    outputs = tuple(o.detach().to("cpu", torch.float32).numpy() for o in sets[0][1])
+    return BenchStats.from_durations(durations, outputs)
+
+
+# ---------------------------------------------------------------------------
+# devices and pools
+# ---------------------------------------------------------------------------
+def _external_device_ids() -> list[int] | None:
+    """Absolute GPU ids from a caller-set HIP_VISIBLE_DEVICES ("2", "0,3",
+    "4-7"), or None when unset or blank."""
+    raw = os.environ.get("HIP_VISIBLE_DEVICES", "").strip()
+    if not raw:
+        return None
+    ids: list[int] = []
+    for part in raw.split(","):
+        lo, _, hi = part.partition("-")
+        ids.extend(range(int(lo), int(hi or lo) + 1))
+    return ids
+
+
+def _visible_gpu_count() -> int:
+    """GPUs this process may use, counted without initialising HIP."""
+    ext = _external_device_ids()
+    if ext is not None:
+        return max(1, len(ext))
+    try:
+        import torch
+
+        return max(1, int(torch.cuda.device_count()))
+    except Exception:
+        return 1
+
+
+def _make_pipeline_pools(
+    *, n_compile: int, core_specs: Sequence
+) -> tuple[Executor, list[Executor]]:
+    """The compile pool plus one single-worker device pool per GPU. Spawned
+    (not forked): each device worker imports torch under its own pin."""
+    ctx = multiprocessing.get_context("spawn")
+    compile_pool = ProcessPoolExecutor(
+        max_workers=n_compile, initializer=_init_compile_worker, mp_context=ctx
+    )
+    device_pools: list[Executor] = [
+        ProcessPoolExecutor(
+            max_workers=1, initializer=_init_visible_devices, initargs=(spec,), mp_context=ctx
+        )
+        for spec in core_specs
+    ]
+    return compile_pool, device_pools
+
+
+# ---------------------------------------------------------------------------
+# durable result store
+# ---------------------------------------------------------------------------
+def clear_stale_artifacts(paths: RunPaths) -> None:
+    """Remove every per-key artefact dir under the run dir (unless
+    AXON_KEEP_NEFF=1 asks to keep them)."""
+    if os.environ.get("AXON_KEEP_NEFF") == "1":
+        return
+    for d in sorted(paths.run_dir.glob("__v*_tiles_*")):
+        if d.is_dir():
+            shutil.rmtree(d, ignore_errors=True)
+
+
+def _append_csv(df, path) -> None:
+    if df.empty:
+        return
+    if not os.path.exists(path):
+        df.to_csv(path, index=False)
+        return
+    import pandas as pd
+
+    have = list(pd.read_csv(path, nrows=0).columns)
+    assert have == list(df.columns), (
+        f"column drift on {path}: existing {have} != new {list(df.columns)}; "
+        f"delete the file to start fresh."
+    )
+    df.to_csv(path, mode="a", header=False, index=False)
+
+
+def tile_cols(tile_args: Sequence[str]) -> list[str]:
+    """CSV column per tile arg: TILES_IN_BLOCK_M -> TILES_M."""
+    return [
+        "TILES_" + a.upper().replace("TILES_IN_BLOCK_", "").replace("TILES_", "")
+        for a in tile_args
+    ]
+
+
+STATS_COLS = ["mean_ms", "median_ms", "min_ms", "max_ms", "std_dev_ms"]
+KEY_PREFIX_COLS = ["lnc", "sharding", "hw_variant", "tile_variant"]
+
+
+def result_columns(spec: KernelSpec) -> list[str]:
+    return [
+        *spec.dim_vars,
+        *KEY_PREFIX_COLS,
+        *tile_cols(spec.tile_args),
+        *STATS_COLS,
+        "correct",
+        "max_abs_err",
+        "error",
+        "mode",
+    ]
+
+
+def key_columns(spec: KernelSpec) -> list[str]:
+    return [*KEY_PREFIX_COLS, *tile_cols(spec.tile_args)]
+
+
+ResultKey = tuple[str, ...]
+
+
+def _truncate_torn_tail(path: Path) -> None:
+    """A record is durable once its newline is on disk; drop anything after
+    the last newline (an append cut short by a kill)."""
+    with path.open("rb+") as f:
+        f.seek(-1, os.SEEK_END)
+        if f.read(1) == b"\n":
+            return
+        f.seek(0)
+        data = f.read()
+        f.seek(0)
+        f.truncate(data.rfind(b"\n") + 1)
+
+
+def read_result_keys(spec: KernelSpec, path: Path) -> set[ResultKey]:
+    """Key of every complete record; asserts on column drift, malformed
+    records and duplicate keys."""
+    if not path.is_file() or path.stat().st_size == 0:
+        return set()
+    _truncate_torn_tail(path)
+    columns = result_columns(spec)
+    idx = [columns.index(c) for c in key_columns(spec)]
+    keys: set[ResultKey] = set()
+    with path.open(newline="") as f:
+        reader = csv.reader(f)
+        header = next(reader, None)
+        if header is None:
+            return set()
+        assert header == columns, (
+            f"column drift on {path}: found {header} != expected {columns}; "
+            f"delete {path.parent} to start fresh."
+        )
+        for lineno, record in enumerate(reader, start=2):
+            assert len(record) == len(columns), (
+                f"malformed record at {path}:{lineno}: {len(record)} fields, "
+                f"expected {len(columns)}; delete {path.parent} to start fresh."
+            )
+            key = tuple(record[i] for i in idx)
+            assert key not in keys, (
+                f"duplicate key {key} at {path}:{lineno}; delete {path.parent} to start fresh."
+            )
+            keys.add(key)
+    return keys
+
+
+def _append_result_row(
+    path: Path, columns: Sequence[str], row: dict, artifact_dir: str | None
+) -> None:
+    """fsync one terminal record, and only then remove the key's artefacts."""
+    path.parent.mkdir(parents=True, exist_ok=True)
+    fresh = not path.exists() or path.stat().st_size == 0
+    buf = io.StringIO()
+    w = csv.writer(buf, lineterminator="\n")
+    if fresh:
+        w.writerow(columns)
+    # One record per physical line: fold any line breaks in error text.
+    w.writerow(["" if row[c] is None else " ".join(str(row[c]).split()) for c in columns])
+    with path.open("a", newline="") as f:
+        f.write(buf.getvalue())
+        f.flush()
+        os.fsync(f.fileno())
+    if artifact_dir and os.environ.get("AXON_KEEP_NEFF") != "1":
+        shutil.rmtree(artifact_dir, ignore_errors=True)
+
+
+def publish_results(spec: KernelSpec, paths: RunPaths, expected_keys: set[ResultKey]) -> None:
+    """Copy the store to the case CSV, only when it holds exactly one
+    terminal row per expected key."""
+    if not expected_keys:
+        return
+    have = read_result_keys(spec, paths.results)
+    missing = sorted(expected_keys - have)
+    extra = sorted(have - expected_keys)
+    assert not missing and not extra, (
+        f"{spec.name}: {paths.results} does not cover the run: "
+        f"{len(missing)} missing key(s) {missing[:5]}, "
+        f"{len(extra)} unexpected key(s) {extra[:5]}"
+    )
+    tmp = paths.csv.with_name(paths.csv.name + ".publish.tmp")
+    shutil.copyfile(paths.results, tmp)
+    os.replace(tmp, paths.csv)
+    print(f"\npublished {len(expected_keys)} row(s) to {paths.csv}")
+
+
+def _ordered_sizes(spec: KernelSpec, dim_sizes: dict[str, int]):
+    return spec.dim_vars, tuple(dim_sizes[d] for d in spec.dim_vars)
+
+
+# ---------------------------------------------------------------------------
+# streaming pipeline
+# ---------------------------------------------------------------------------
+def _stream_compile_bench(
+    tasks: Sequence[tuple[tuple[int, ...], tuple, tuple]],
+    *,
+    n_compile: int,
+    core_specs: Sequence,
+    max_live: int,
+    desc: str,
+) -> Iterator[tuple[tuple[int, ...], BenchResult, str]]:
+    """Yield one (key, result, artifact_dir) per task. At most `max_live`
+    tasks sit between submission and their yield; a device is handed the
+    next compiled task as soon as it frees up."""
+    from tqdm import tqdm
+
+    compile_pool, device_pools = _make_pipeline_pools(n_compile=n_compile, core_specs=core_specs)
+    idle: deque[Executor] = deque(device_pools)
+    ready: deque[tuple] = deque()
+    compiling: dict[Any, tuple] = {}
+    benching: dict[Any, tuple[tuple, Executor]] = {}
+    pending = iter(tasks)
+    bar = tqdm(total=len(tasks), desc=desc)
+    try:
+        while True:
+            while len(compiling) + len(ready) + len(benching) < max_live:
+                task = next(pending, None)
+                if task is None:
+                    break
+                compiling[compile_pool.submit(_compile_one_variant, task[1])] = task
+            while idle and ready:
+                task = ready.popleft()
+                pool = idle.popleft()
+                benching[pool.submit(_bench_one_artifact, task[2])] = (task, pool)
+            if not compiling and not benching:
+                return
+            done, _ = wait(set(compiling) | set(benching), return_when=FIRST_COMPLETED)
+            for fut in done:
+                if fut in compiling:
+                    task = compiling.pop(fut)
+                    try:
+                        _, artifact, err = fut.result()
+                    except Exception as e:  # worker died / unpicklable payload
+                        artifact, err = None, f"{type(e).__name__}: {e}"
+                    if artifact is not None:
+                        ready.append(task)
+                        continue
+                    bar.update(1)
+                    yield (
+                        task[0],
+                        BenchError(message=f"compile: {err or 'artifact_missing'}"),
+                        os.path.dirname(task[1][5]),
+                    )
+                else:
+                    task, pool = benching.pop(fut)
+                    idle.append(pool)
+                    try:
+                        result: BenchResult = fut.result()
+                    except Exception as e:
+                        bar.write(f"Error benchmarking HIP tiles {task[0]}: {e}")
+                        result = BenchError.from_exception(e)
+                    bar.update(1)
+                    yield task[0], result, os.path.dirname(task[1][5])
+    finally:
+        bar.close()
+        compile_pool.shutdown(wait=False, cancel_futures=True)
+        for pool in device_pools:
+            pool.shutdown(wait=False, cancel_futures=True)
+
+
+def _compute_ref_outputs(baseline_op, inputs: tuple) -> tuple[np.ndarray, ...] | None:
+    """`baseline_op` on fp32-upcast inputs, as a tuple of fp32 arrays."""
+    if baseline_op is None:
+        return None
+    out = baseline_op(*[_dt.to_f32_numpy(a) for a in inputs])
+    outs = out if isinstance(out, tuple) else (tuple(out) if isinstance(out, list) else (out,))
+    return tuple(np.asarray(o, dtype=np.float32) for o in outs)
+
+
+def _compute_torch_ref_outputs(torch_ref, inputs: tuple) -> tuple[np.ndarray, ...] | None:
+    """`torch_ref` on fp32 torch inputs (the harness convention,
+    src/axon/case_gen.py:190-226), as a tuple of fp32 arrays."""
+    if torch_ref is None:
+        return None
+    import torch
+
+    with torch.no_grad():
+        out = torch_ref(*[_dt.to_f32_torch(a) for a in inputs])
+    outs = out if isinstance(out, tuple) else (out,)
+    return tuple(o.detach().to(torch.float32).numpy() for o in outs)
+
+
+def _input_dtype_codes(inputs: Sequence[Any]) -> tuple[int, ...]:
+    codes = []
+    for a in inputs:
+        if _dt.is_bf16(a):
+            codes.append(0)
+        else:
+            t = _dt.to_torch(a)
+            import torch
+
+            table = {torch.float16: 1, torch.float32: 2}
+            if t.dtype not in table:
+                raise ValueError(f"unsupported input dtype {t.dtype}")
+            codes.append(table[t.dtype])
+    return tuple(codes)
+
+
+def run_hip_bench(
+    spec: KernelSpec,
+    dim_sizes: dict[str, int],
+    *,
+    hw_variant: int,
+    tile_variant: int,
+    module_path: str,
+    function_name: str,
+    warmup: int,
+    bench: int,
+    paths: RunPaths,
+    target: str | None = None,
+    dtype: Any | None = None,
+    rtol: float,
+    atol: float,
+    lnc: int = 1,
+    sharding: str = "lnc1",
+    candidate_filter: bool = True,
+    candidate_budget: int = 8,
+    candidate_seed: int = SEED,
+) -> set[ResultKey]:
+    """Compile + bench every selected tile tuple of one variant module,
+    appending one terminal row per key to `paths.results`. Returns this
+    call's expected key set (for `publish_results`)."""
+    print("\n" + "=" * 80)
+    print(
+        f"HIP {spec.name.upper()} BENCHMARK (hw_variant={hw_variant}, "
+        f"tile_variant={tile_variant}, lnc={lnc}, sharding={sharding})"
+    )
+    print("=" * 80)
+
+    inputs = spec.make_inputs(
+        **dim_sizes, **({"dtype": dtype} if dtype is not None else {}),
+        rng=np.random.default_rng(SEED),
+    )
+    ordered_dims, ordered_sizes = _ordered_sizes(spec, dim_sizes)
+    all_keys = list(product(spec.tile_options, repeat=len(spec.tile_args)))
+    if candidate_filter:
+        constraints = read_manifest(module_path)
+        if constraints:
+            n_source = len(all_keys)
+            legal = [k for k in all_keys if rejection_reason(spec.tile_args, k, constraints) is None]
+            all_keys = select_diverse(legal, budget=candidate_budget, seed=candidate_seed)
+            print(
+                f"\ncandidate filter: {n_source} source -> {len(legal)} legal -> "
+                f"{len(all_keys)} selected (budget={candidate_budget or 'unlimited'})"
+            )
+    tcols = tile_cols(spec.tile_args)
+    columns = result_columns(spec)
+    key_idx = [columns.index(c) for c in key_columns(spec)]
+
+    def _row(tile_values, *, stats=None, correct=None, max_abs_err=None, error=None, mode=None):
+        timing = (
+            {k: v for k, v in asdict(stats).items() if k != "outputs"}
+            if stats is not None
+            else dict.fromkeys(STATS_COLS)
+        )
+        return {
+            **dict(zip(ordered_dims, ordered_sizes, strict=True)),
+            "lnc": lnc,
+            "sharding": sharding,
+            "hw_variant": hw_variant,
+            "tile_variant": tile_variant,
+            **dict(zip(tcols, tile_values, strict=True)),
+            **timing,
+            "correct": correct,
+            "max_abs_err": max_abs_err,
+            "error": error,
+            "mode": mode,
+        }
+
+    def _key(tile_values) -> ResultKey:
+        row = _row(tile_values)
+        return tuple(str(row[columns[i]]) for i in key_idx)
+
+    expected = {_key(tv) for tv in all_keys}
+    paths.run_dir.mkdir(parents=True, exist_ok=True)
+    done = read_result_keys(spec, paths.results)
+    todo = [tv for tv in all_keys if _key(tv) not in done]
+    if todo != all_keys:
+        print(f"\nresuming: {len(all_keys) - len(todo)}/{len(all_keys)} key(s) already terminal")
+
+    def _terminal(tile_values, artifact_dir, **kw) -> None:
+        _append_result_row(paths.results, columns, _row(tile_values, **kw), artifact_dir)
+
+    n_gpus = _visible_gpu_count()
+    if lnc > 1:
+        msg = f"lnc={lnc}: multi-device sharding is not part of this backend; skipping {spec.name}"
+        print(f"\n[skip] {msg}")
+        clear_stale_artifacts(paths)
+        for tv in todo:
+            _terminal(tv, None, error=msg)
+        return expected
+
+    ref_outputs = _compute_ref_outputs(spec.baseline_op, inputs)
+    torch_outputs = _compute_torch_ref_outputs(spec.torch_ref, inputs)
+
+    def _check(outputs) -> tuple[bool | None, float | None]:
+        refs = [r for r in (ref_outputs, torch_outputs) if r is not None]
+        if not refs or outputs is None:
+            return None, None
+        errs, oks = [], []
+        for ref in refs:
+            for got, want in zip(outputs, ref, strict=True):
+                g = np.asarray(got, dtype=np.float32)
+                if g.shape != want.shape:
+                    return False, float("inf")
+                with np.errstate(invalid="ignore"):
+                    errs.append(float(np.abs(g - want).max()) if g.size else 0.0)
+                oks.append(bool(np.allclose(g, want, rtol=rtol, atol=atol)))
+        return all(oks), max(errs)
+
+    clear_stale_artifacts(paths)
+
+    ids = _external_device_ids() or list(range(n_gpus))
+    device_specs: list = list(ids)
+    max_live = int(os.environ.get("AXON_MAX_LIVE_NEFFS") or 0) or max(4, 2 * len(device_specs))
+    n_compile = int(os.environ.get("AXON_COMPILE_WORKERS") or 0) or max(
+        1, min(8, multiprocessing.cpu_count() // 2)
+    )
+    print(
+        f"\nStreaming {len(todo)} key(s): {n_compile} compile worker(s) (AXON_COMPILE_WORKERS) "
+        f"-> {len(device_specs)} device worker(s), <= {max_live} live artefact dir(s) "
+        f"(AXON_MAX_LIVE_NEFFS)"
+    )
+
+    dims = tuple(int(dim_sizes[d]) for d in spec.dim_vars)
+    codes = _input_dtype_codes(inputs)
+    tasks = []
+    for tv in todo:
+        art = str(paths.artifact(hw_variant, tile_variant, tv))
+        tile_kwargs = dict(zip(spec.tile_args, tv, strict=True))
+        tasks.append(
+            (
+                tv,
+                (module_path, function_name, tv, (dims, codes), tile_kwargs, art,
+                 target or DEFAULT_TARGET, lnc),
+                (module_path, function_name, tv, tuple(spec.tile_args), inputs, art, warmup, bench),
+            )
+        )
+
+    n_failed = n_wrong = 0
+    err_counts: Counter[str] = Counter()
+    for tv, result, artifact_dir in _stream_compile_bench(
+        tasks,
+        n_compile=n_compile,
+        core_specs=device_specs,
+        max_live=max_live,
+        desc=f"HIP {spec.name} v{hw_variant}t{tile_variant}",
+    ):
+        if isinstance(result, BenchError):
+            _terminal(tv, artifact_dir, error=result.message)
+            err_counts[result.message.split(":")[0]] += 1
+            n_failed += 1
+        else:
+            correct, err = _check(result.outputs)
+            n_wrong += (not correct) if correct is not None else 0
+            _terminal(tv, artifact_dir, stats=result, correct=correct, max_abs_err=err)
+
+    if n_failed:
+        print(f"\n[warn] {n_failed}/{len(todo)} key(s) for {spec.name} failed; see `error` in {paths.results}")
+        for tag, count in err_counts.most_common():
+            print(f"  {count:4d}  {tag}")
+    if n_wrong:
+        print(
+            f"\n[warn] {n_wrong}/{len(todo)} bench runs for {spec.name} failed correctness "
+            f"(rtol={rtol}, atol={atol})"
+        )
+    print(f"\n{spec.name} rows appended to {paths.results}")
+    return expected
+
+
+# The reference's name for the same entry point.
+run_nki_bench = run_hip_bench
+
+
+def time_cpu_reference(fn, inputs, *, warmup: int = 3, runs: int = 10, threads: int | None = None):
+    """Median wall time (ms) of `fn(*fp32 torch inputs)` on the host cores,
+    with the thread count used. The CPU baseline of a spec is its
+    `torch_ref` timed this way."""
+    import torch
+
+    n = threads or len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    args = [_dt.to_f32_torch(a) for a in inputs]
+    with torch.no_grad():
+        for _ in range(warmup):
+            fn(*args)
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn(*args)
+            times.append((time.perf_counter() - t0) * 1e3)
+    return BenchStats.from_durations(times), torch.get_num_threads()
+
+
+def run_baseline(
+    spec: KernelSpec,
+    dim_sizes: dict[str, int],
+    *,
+    warmup: int,
+    bench: int,
+    paths: RunPaths,
+    target: str | None = None,
+    dtype: Any | None = None,
+) -> str:
+    """`--mode baseline`: the spec's `torch_ref` (or `baseline_op`) timed on
+    the host CPU cores, appended to the baseline CSV (the reference times a
+    numpy-on-device baseline here, src/axon/bench_runner.py:828-889)."""
+    del target
+    fn = spec.torch_ref
+    if fn is None and spec.baseline_op is None:
+        raise ValueError(f"kernel '{spec.name}' has no baseline_op set")
+    import pandas as pd
+
+    print("\n" + "=" * 80)
+    print(f"CPU TORCH BASELINE {spec.name.upper()}")
+    print("=" * 80)
+    ordered_dims, ordered_sizes = _ordered_sizes(spec, dim_sizes)
+    paths.baseline_dir.mkdir(parents=True, exist_ok=True)
+    inputs = spec.make_inputs(
+        **dim_sizes, **({"dtype": dtype} if dtype is not None else {}),
+        rng=np.random.default_rng(SEED),
+    )
+    if fn is None:
+        base = spec.baseline_op
+
+        def fn(*xs):
+            return base(*[x.numpy() for x in xs])
+
+    stats, threads = time_cpu_reference(fn, inputs, warmup=max(1, warmup), runs=max(1, bench))
+    row = {
+        **{k: v for k, v in asdict(stats).items() if k != "outputs"},
+        **dict(zip(ordered_dims, ordered_sizes, strict=True)),
+        "cpu_threads": threads,
+    }
+    df = pd.DataFrame([row])
+    print(f"\nBaseline {spec.name} Results:")
+    print(df.to_string(index=False))
+    _append_csv(df, str(paths.baseline_csv))
+    print(f"\n{spec.name} baseline appended to {paths.baseline_csv}")
+    return str(paths.baseline_csv)
