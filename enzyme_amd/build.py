@@ -2,8 +2,8 @@
 
 Each `csrc/*.hip` file is compiled to an object in `_build/` with hipcc, in
 parallel, then linked into `enzyme_amd/lib/libaxon_hip.so`. Per-file extra
-flags live in `EXTRA_FLAGS` (the fused-Adam unit is built without FMA
-contraction so its arithmetic rounds like the fp32 CPU reference).
+flags live in `EXTRA_FLAGS` (the elementwise unit, which holds fused Adam, is built without
+FMA contraction so its arithmetic rounds like the fp32 CPU reference).
 
 Run `python -m enzyme_amd.build` (or `__graft_entry__.build()`).
 """
@@ -45,7 +45,7 @@ COMMON_FLAGS = [
 ]
 
 EXTRA_FLAGS: dict[str, list[str]] = {
-    "adam.hip": ["-ffp-contract=off"],
+    "elementwise.hip": ["-ffp-contract=off"],
 }
 
 

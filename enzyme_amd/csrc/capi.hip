@@ -13,15 +13,19 @@ const Family* family_rmsnorm();
 const Family* family_rmsnorm_weighted();
 const Family* family_layernorm();
 const Family* family_softmax();
+const Family* family_rope();
+const Family* family_rope_llama3();
+const Family* family_fused_adam();
+const Family* family_cumsum();
+const Family* family_cumsum_probs();
 
 namespace {
 
 using FamilyFn = const Family* (*)();
 const FamilyFn kFamilyFns[] = {
-    family_rmsnorm,
-    family_rmsnorm_weighted,
-    family_layernorm,
-    family_softmax,
+    family_rmsnorm,     family_rmsnorm_weighted, family_layernorm, family_softmax,
+    family_rope,        family_rope_llama3,      family_fused_adam, family_cumsum,
+    family_cumsum_probs,
 };
 constexpr int kNumFamilies = sizeof(kFamilyFns) / sizeof(kFamilyFns[0]);
 

@@ -1,0 +1,56 @@
+"""GPU parity driver shared by the test_gpu_* modules: launch a spec's HIP
+family through the C ABI for a set of tile tuples and compare each output
+with the oracle on the same seeded inputs."""
+
+from __future__ import annotations
+
+from itertools import product
+
+import torch
+
+import oracle
+from enzyme_amd import hip
+from enzyme_amd.candidate_filter import select_diverse
+from tests._specs import as_tuple, spec_inputs, to_device
+
+
+def legal_tiles(name, variant, dims, codes, n_tiles, options=(1, 2, 4, 8, 16, 32)):
+    out = []
+    for t in product(options, repeat=n_tiles):
+        if hip.check(name, variant, t, dims, codes)[0] == hip.AXON_OK:
+            out.append(t)
+    return out
+
+
+def check_parity(name, sizes, *, rtol, atol, variants=None, budget=0, dtype=None,
+                 want=None, seed=42):
+    """Returns the number of (variant, tiles) keys checked; raises on the first
+    mismatch (message names the key)."""
+    spec, dims, host = spec_inputs(name, sizes, dtype=dtype, seed=seed)
+    dev = to_device(host)
+    codes = [hip.dtype_code(t) for t in dev]
+    dvals = [dims[d] for d in spec.dim_vars]
+    if want is None:
+        want = as_tuple(oracle.ORACLE[name](*[t.cpu() for t in dev]))
+    variants = range(hip.variant_count(name)) if variants is None else variants
+    checked = 0
+    for v in variants:
+        tiles = legal_tiles(name, v, dvals, codes, len(spec.tile_args))
+        assert tiles, f"{name} v{v}: no legal tile tuple for {sizes}"
+        if budget:
+            tiles = select_diverse(tiles, budget=budget, seed=42)
+        for t in tiles:
+            ln = hip.Launcher(name, v, t, dvals, dev, input_shapes=spec.input_shapes(dims))
+            for o in ln.outputs:
+                o.fill_(float("nan"))
+            ln.launch()
+            torch.cuda.synchronize()
+            for i, (got, ref) in enumerate(zip(ln.outputs, want)):
+                g = got.float().cpu()
+                assert torch.isfinite(g).all(), f"{name} v{v} tiles {t} out{i}: non-finite"
+                torch.testing.assert_close(
+                    g, ref.float(), rtol=rtol, atol=atol,
+                    msg=lambda m, v=v, t=t, i=i: f"{name} v{v} tiles {t} out{i}: {m}",
+                )
+            checked += 1
+    return checked
