@@ -1,0 +1,470 @@
+// Flash attention with bf16 MFMA and an online fp32 softmax.
+//
+//   attention_causal  O = softmax(Q K^T / sqrt(d) + causal mask) V over
+//                     [b, h, s, d] tensors (Q, K, V, O all [b, h, s, d] bf16)
+//   attention_nkilib  O = softmax(q @ k_t) V, single head: q [s, d],
+//                     k_t [d, s] (K given transposed), v [s, d], no scale,
+//                     no mask (kernels/attention_nkilib/kernel.py:14-21; the
+//                     reference's bare exp/sum equals the max-shifted softmax
+//                     used here)
+//
+// Schedule (hw variant 0): a workgroup of W waves owns 32*W query rows of one
+// (batch, head); each wave owns 32 of them and walks the key/value sequence
+// in blocks of BKV keys staged through double-buffered LDS (K as [key][d],
+// V transposed as [d][key]).
+// Per block a wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (Q^T
+// held in registers for the whole walk), so each lane holds the scores of
+// ONE query (lane % 32) for 16 keys per 32-key tile: the row max and row
+// sum are in-lane reductions plus one exchange with lane ^ 32. The
+// probabilities P^T = exp2(S^T - m) are converted to bf16 in place and are
+// directly the B operand of O^T = V^T P^T; the MFMA's k index is mapped to
+// keys {0-3, 8-11 | 4-7, 12-15} (+16) to match the accumulator layout, and
+// V^T is read from LDS with the same key mapping. O^T keeps one query per
+// lane too, so the online-softmax rescale is a per-lane multiply.
+// Causal: key blocks past a wave's last query are skipped, only the diagonal
+// block is masked, and the heaviest query blocks are scheduled first.
+// Tile arguments: TILES_IN_BLOCK_M = W (waves, 32 queries each),
+//                 TILES_IN_BLOCK_N = BKV / 32; K and P are pinned to 1.
+#include <atomic>
+
+#include "common.hpp"
+#include "registry.hpp"
+
+namespace axon {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int D = 128;
+constexpr int KP = D + 8;  // Ks row pitch (elements)
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnArgs {
+  const bf16* q;   // [BH][s][D]
+  const bf16* k;   // [BH][s][D], or k_t [D][s] when KT
+  const bf16* v;   // [BH][s][D]
+  bf16* o;         // [BH][s][D]
+  int s;
+  int bh;
+  int qblocks;
+  float scale_log2;  // softmax scale * log2(e)
+};
+
+template <int W, int TN, bool CAUSAL, bool KT>
+__global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
+  constexpr int BQ = 32 * W;
+  constexpr int BKV = 32 * TN;
+  constexpr int VP = BKV + 8;         // Vt row pitch (elements)
+  constexpr int NT = W * 64;
+  constexpr int KR = BKV / (4 * W);   // keys (or d rows) per thread per block load
+  static_assert(KR >= 1 && KR <= 8, "tile shape");
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* Ks = reinterpret_cast<bf16*>(smem);  // [2][BKV][KP]
+  bf16* Vt = Ks + 2 * BKV * KP;              // [2][D][VP]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = lane >> 5;  // half of the wave
+
+  // Heaviest (latest) query blocks first under causal masking.
+  const int qb = CAUSAL ? (a.qblocks - 1 - static_cast<int>(blockIdx.x) % a.qblocks)
+                        : static_cast<int>(blockIdx.x) % a.qblocks;
+  const int bh = static_cast<int>(blockIdx.x) / a.qblocks;
+  const int64_t base = static_cast<int64_t>(bh) * a.s * D;
+  const bf16* Q = a.q + base;
+  const bf16* K = a.k + base;
+  const bf16* V = a.v + base;
+  bf16* O = a.o + base;
+
+  const int q0 = qb * BQ;
+  const int qw = q0 + wave * 32;  // this wave's first query
+  const int my_q = qw + (lane & 31);
+  const int kv_end = CAUSAL ? min(a.s, q0 + BQ) : a.s;
+  const int nblocks = (kv_end + BKV - 1) / BKV;
+
+  // Q^T fragments (B operand): lane holds Q[my_q][step*16 + h*8 .. +8].
+  bf16x8 qf[D / 16];
+#pragma unroll
+  for (int st = 0; st < D / 16; ++st) {
+    if (my_q < a.s)
+      qf[st] = *reinterpret_cast<const bf16x8*>(Q + static_cast<int64_t>(my_q) * D + st * 16 + h * 8);
+    else
+      for (int i = 0; i < 8; ++i) qf[st][i] = static_cast<bf16>(0.f);
+  }
+
+  // Global -> register staging of one K/V block.
+  Vec<bf16> kreg[KR], vreg[KR];
+  // K (row layout [key][d]): vector v = tid + i*NT -> key v/16, d chunk v%16.
+  // K^T layout [d][key]: thread -> d rows (tid % (D/KR))*KR.., keys chunk
+  //   (tid / (D/KR))*8 .. +8 -- transposed into Ks on store.
+  // V: thread -> keys (tid / 16)*KR .. +KR, d chunk (tid % 16)*8.
+  auto load_block = [&](int kv0) {
+#pragma unroll
+    for (int i = 0; i < KR; ++i) {
+      if constexpr (!KT) {
+        const int v = tid + i * NT;
+        const int key = kv0 + (v >> 4), dc = (v & 15) * 8;
+        if (key < a.s) kreg[i] = load_vec(K + static_cast<int64_t>(key) * D + dc);
+        else for (int e = 0; e < 8; ++e) kreg[i].v[e] = static_cast<bf16>(0.f);
+      } else {
+        const int dr = (tid % (D / KR)) * KR + i;
+        const int key = kv0 + (tid / (D / KR)) * 8;
+        if (key + 7 < a.s) {
+          kreg[i] = load_vec(K + static_cast<int64_t>(dr) * a.s + key);
+        } else {
+          for (int e = 0; e < 8; ++e)
+            kreg[i].v[e] = key + e < a.s ? K[static_cast<int64_t>(dr) * a.s + key + e] : static_cast<bf16>(0.f);
+        }
+      }
+      const int key = kv0 + (tid >> 4) * KR + i;
+      const int dc = (tid & 15) * 8;
+      if (key < a.s) vreg[i] = load_vec(V + static_cast<int64_t>(key) * D + dc);
+      else for (int e = 0; e < 8; ++e) vreg[i].v[e] = static_cast<bf16>(0.f);
+    }
+  };
+
+  auto store_block = [&](int buf) {
+    bf16* ks = Ks + buf * BKV * KP;
+    bf16* vt = Vt + buf * D * VP;
+    if constexpr (!KT) {
+#pragma unroll
+      for (int i = 0; i < KR; ++i) {
+        const int v = tid + i * NT;
+        store_vec(ks + (v >> 4) * KP + (v & 15) * 8, kreg[i]);
+      }
+    } else {
+      // kreg[i] holds d row dr0+i for keys kc..kc+7: write each key's KR d-values.
+      const int dr0 = (tid % (D / KR)) * KR;
+      const int kc = (tid / (D / KR)) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int i = 0; i < KR; ++i) ks[(kc + e) * KP + dr0 + i] = kreg[i].v[e];
+    }
+    // V transposed: d row dc+e gets keys kb..kb+KR-1.
+    const int kb = (tid >> 4) * KR;
+    const int dc = (tid & 15) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int i = 0; i < KR; ++i) vt[(dc + e) * VP + kb + i] = vreg[i].v[e];
+  };
+
+  floatx16 acc_o[D / 32];
+#pragma unroll
+  for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc_o[t][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  if (nblocks > 0) {
+    load_block(0);
+    store_block(0);
+  }
+  __syncthreads();
+
+  for (int blk = 0; blk < nblocks; ++blk) {
+    const int buf = blk & 1;
+    const int kv0 = blk * BKV;
+    if (blk + 1 < nblocks) load_block(kv0 + BKV);
+
+    const bool active = !CAUSAL || kv0 <= qw + 31;
+    if (active && qw < a.s) {
+      const bf16* ks = Ks + buf * BKV * KP;
+      const bf16* vt = Vt + buf * D * VP;
+      // S^T = K Q^T: acc_s[t] rows = keys t*32.., columns = this wave's queries.
+      floatx16 acc_s[TN];
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_s[t][e] = 0.f;
+#pragma unroll
+        for (int st = 0; st < D / 16; ++st) {
+          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + (t * 32 + (lane & 31)) * KP + st * 16 + h * 8);
+          acc_s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], acc_s[t], 0, 0, 0);
+        }
+      }
+      // Scale, mask, block max for this lane's query.
+      const bool diag = CAUSAL && kv0 + BKV - 1 > qw;
+      float mblk = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kv0 + t * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+          float x = acc_s[t][e] * a.scale_log2;
+          if ((diag && key > my_q) || key >= a.s) x = -INFINITY;
+          acc_s[t][e] = x;
+          mblk = fmaxf(mblk, x);
+        }
+      mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
+      const float m_new = fmaxf(m_run, mblk);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m_run - m_use);
+      float lblk = 0.f;
+      // P^T in bf16, grouped by MFMA k-step: pf[t][ks] holds keys
+      // t*32 + ks*16 + {0-3, 8-11} (h = 0) or {4-7, 12-15} (h = 1).
+      bf16x8 pf[TN][2];
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float p = exp2f(acc_s[t][e] - m_use);
+          lblk += p;
+          pf[t][e >> 3][e & 7] = static_cast<bf16>(p);
+        }
+      lblk += __shfl_xor(lblk, 32, 64);
+      l_run = l_run * alpha + lblk;
+      m_run = m_new;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_o[dt][e] *= alpha;
+      // O^T += V^T P^T.
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int ks2 = 0; ks2 < 2; ++ks2) {
+          const int kb = t * 32 + ks2 * 16 + 4 * h;
+#pragma unroll
+          for (int dt = 0; dt < D / 32; ++dt) {
+            const bf16* row = vt + (dt * 32 + (lane & 31)) * VP + kb;
+            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row);
+            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 8);
+            bf16x8 vf;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              vf[i] = lo[i];
+              vf[4 + i] = hi[i];
+            }
+            acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][ks2], acc_o[dt], 0, 0, 0);
+          }
+        }
+    }
+    // The other buffer was last read before the previous barrier.
+    if (blk + 1 < nblocks) store_block(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (my_q < a.s) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        bf16x4 out;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[i] = static_cast<bf16>(acc_o[dt][g4 * 4 + i] * inv);
+        const int d = dt * 32 + 8 * g4 + 4 * h;
+        *reinterpret_cast<bf16x4*>(O + static_cast<int64_t>(my_q) * D + d) = out;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+const char* const kTileArgs[] = {"TILES_IN_BLOCK_M", "TILES_IN_BLOCK_N", "TILES_IN_BLOCK_K",
+                                 "TILES_IN_BLOCK_P"};
+
+size_t attn_lds(int TN) {
+  const int BKV = 32 * TN;
+  return static_cast<size_t>(2) * (BKV * KP + D * (BKV + 8)) * sizeof(bf16);
+}
+
+int check_tiles(const Call& c, std::string* why) {
+  const int W = c.tile(0), TN = c.tile(1);
+  if (!(W == 1 || W == 2 || W == 4 || W == 8)) {
+    *why = "TILES_IN_BLOCK_M (waves of 32 queries) must be 1, 2, 4 or 8";
+    return AXON_EINVAL;
+  }
+  if (!(TN == 1 || TN == 2 || TN == 4)) {
+    *why = "TILES_IN_BLOCK_N (key block / 32) must be 1, 2 or 4";
+    return AXON_EINVAL;
+  }
+  // Each thread stages KR = BKV / (4 W) keys (or k_t rows) per block.
+  if (32 * TN % (4 * W) != 0 || 32 * TN / (4 * W) > 8) {
+    *why = "the key block must satisfy 4 x waves <= BKV <= 32 x waves";
+    return AXON_EINVAL;
+  }
+  if (c.tile(2) != 1 || c.tile(3) != 1) {
+    *why = "TILES_IN_BLOCK_K and TILES_IN_BLOCK_P are unused and must be 1";
+    return AXON_EINVAL;
+  }
+  return AXON_OK;
+}
+
+// attention_causal: dims b, h, s, d
+int check_causal(const Call& c, std::string* why) {
+  if (c.n_tiles != 4 || c.n_dims != 4 || c.n_dtypes != 3) {
+    *why = "expected 4 tiles, 4 dims (b, h, s, d) and 3 dtypes";
+    return AXON_EARG;
+  }
+  for (int i = 0; i < 3; ++i)
+    if (c.dtype(i) != AXON_BF16) {
+      *why = "bf16 inputs only";
+      return AXON_EDTYPE;
+    }
+  if (c.dim(3) != D) {
+    *why = "head dim must be 128";
+    return AXON_EINVAL;
+  }
+  if (c.dim(0) < 0 || c.dim(1) < 0 || c.dim(2) < 0 || c.dim(0) * c.dim(1) > (1 << 20) ||
+      c.dim(2) > (1 << 24)) {
+    *why = "dimension out of range";
+    return AXON_EINVAL;
+  }
+  return check_tiles(c, why);
+}
+
+// attention_nkilib: dims s, d
+int check_nki(const Call& c, std::string* why) {
+  if (c.n_tiles != 4 || c.n_dims != 2 || c.n_dtypes != 3) {
+    *why = "expected 4 tiles, 2 dims (s, d) and 3 dtypes";
+    return AXON_EARG;
+  }
+  for (int i = 0; i < 3; ++i)
+    if (c.dtype(i) != AXON_BF16) {
+      *why = "bf16 inputs only";
+      return AXON_EDTYPE;
+    }
+  if (c.dim(1) != D) {
+    *why = "head dim must be 128";
+    return AXON_EINVAL;
+  }
+  if (c.dim(0) < 0 || c.dim(0) > (1 << 24)) {
+    *why = "dimension out of range";
+    return AXON_EINVAL;
+  }
+  if (c.dim(0) % 8 != 0) {
+    *why = "s must be a multiple of 8 (16-byte rows of k_t)";
+    return AXON_EINVAL;
+  }
+  return check_tiles(c, why);
+}
+
+int manifest_attn(int, const int64_t* dims, int, Constraint* out, int cap, int64_t s) {
+  (void)dims;
+  if (cap < 4) return 0;
+  const int64_t sq = s > 0 ? s : 1;
+  out[0] = {"TILES_IN_BLOCK_M", 8, 1, false};
+  out[1] = {"TILES_IN_BLOCK_N", sq < 128 ? (sq < 32 ? 32 : sq) : 128, 32, false};
+  out[2] = {"TILES_IN_BLOCK_K", 1, 1, false};
+  out[3] = {"TILES_IN_BLOCK_P", 1, 1, false};
+  return 4;
+}
+
+int manifest_causal(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
+  (void)dt;
+  return manifest_attn(v, dims, dt, out, cap, dims[2]);
+}
+
+int manifest_nki(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
+  (void)dt;
+  return manifest_attn(v, dims, dt, out, cap, dims[0]);
+}
+
+size_t no_workspace(const Call&) { return 0; }
+
+void outputs_causal(const int64_t* dims, const int32_t*, OutDesc* out) {
+  out[0] = {4, {dims[0], dims[1], dims[2], dims[3]}, AXON_BF16};
+}
+
+void outputs_nki(const int64_t* dims, const int32_t*, OutDesc* out) {
+  out[0] = {2, {dims[0], dims[1]}, AXON_BF16};
+}
+
+template <int W, int TN, bool CAUSAL, bool KT>
+int launch_t(const AttnArgs& a, hipStream_t st) {
+  const size_t lds = attn_lds(TN);
+  auto fn = attn_kernel<W, TN, CAUSAL, KT>;
+  static std::atomic<bool> configured{false};
+  if (!configured.load(std::memory_order_acquire)) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                        static_cast<int>(lds));
+    configured.store(true, std::memory_order_release);
+  }
+  const unsigned blocks = static_cast<unsigned>(a.qblocks) * static_cast<unsigned>(a.bh);
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(W * 64), lds, st, a);
+  return launch_status("attn_kernel");
+}
+
+template <bool CAUSAL, bool KT>
+int dispatch(int W, int TN, const AttnArgs& a, hipStream_t st) {
+#define AXON_ATTN_CASE(w, tn) \
+  if (W == w && TN == tn) return launch_t<w, tn, CAUSAL, KT>(a, st);
+  AXON_ATTN_CASE(1, 1)
+  AXON_ATTN_CASE(2, 1) AXON_ATTN_CASE(2, 2)
+  AXON_ATTN_CASE(4, 1) AXON_ATTN_CASE(4, 2) AXON_ATTN_CASE(4, 4)
+  AXON_ATTN_CASE(8, 1) AXON_ATTN_CASE(8, 2) AXON_ATTN_CASE(8, 4)
+#undef AXON_ATTN_CASE
+  set_error("no attention instantiation for this tile");
+  return AXON_EINVAL;
+}
+
+int launch_common(const Call& c, const void* const* in, void* const* out, hipStream_t st, int64_t bh,
+                  int64_t s, bool causal) {
+  if (bh == 0 || s == 0) return AXON_OK;
+  for (int i = 0; i < 3; ++i)
+    if (!aligned16(in[i])) {
+      set_error("attention inputs must be 16-byte aligned");
+      return AXON_EARG;
+    }
+  if (!aligned16(out[0])) {
+    set_error("attention output must be 16-byte aligned");
+    return AXON_EARG;
+  }
+  const int W = c.tile(0), TN = c.tile(1);
+  AttnArgs a;
+  a.q = static_cast<const bf16*>(in[0]);
+  a.k = static_cast<const bf16*>(in[1]);
+  a.v = static_cast<const bf16*>(in[2]);
+  a.o = static_cast<bf16*>(out[0]);
+  a.s = static_cast<int>(s);
+  a.bh = static_cast<int>(bh);
+  a.qblocks = static_cast<int>((s + 32 * W - 1) / (32 * W));
+  if (static_cast<int64_t>(a.qblocks) * a.bh > (1LL << 31) - 1) {
+    set_error("grid too large");
+    return AXON_EINVAL;
+  }
+  if (causal) {
+    a.scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
+    return dispatch<true, false>(W, TN, a, st);
+  }
+  a.scale_log2 = kLog2e;
+  return dispatch<false, true>(W, TN, a, st);
+}
+
+int launch_causal(const Call& c, const void* const* in, void* const* out, void*, hipStream_t st) {
+  return launch_common(c, in, out, st, c.dim(0) * c.dim(1), c.dim(2), true);
+}
+
+int launch_nki(const Call& c, const void* const* in, void* const* out, void*, hipStream_t st) {
+  return launch_common(c, in, out, st, 1, c.dim(0), false);
+}
+
+const char* summary_attn(int) {
+  return "flash attention: S^T = K Q^T on 32x32x16 bf16 MFMA with Q^T in registers, one query per "
+         "lane for an in-lane online softmax (exp2, fp32), P^T kept in registers as the B operand "
+         "of O^T = V^T P^T, K and V^T double-buffered in LDS, causal block skipping";
+}
+
+}  // namespace
+
+const Family* family_attention_causal() {
+  static const Family f = {"attention_causal", 1, 3, 1, 4, kTileArgs, 4, summary_attn,
+                           manifest_causal, check_causal, no_workspace, outputs_causal, launch_causal};
+  return &f;
+}
+
+const Family* family_attention_nkilib() {
+  static const Family f = {"attention_nkilib", 1, 3, 1, 2, kTileArgs, 4, summary_attn, manifest_nki,
+                           check_nki, no_workspace, outputs_nki, launch_nki};
+  return &f;
+}
+
+}  // namespace axon

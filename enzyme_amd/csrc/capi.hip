@@ -18,14 +18,22 @@ const Family* family_rope_llama3();
 const Family* family_fused_adam();
 const Family* family_cumsum();
 const Family* family_cumsum_probs();
+const Family* family_matmul();
+const Family* family_matmul_std002();
+const Family* family_rmsnorm_matmul();
+const Family* family_rmsnorm_matmul_eps();
+const Family* family_silu_mlp();
+const Family* family_attention_causal();
+const Family* family_attention_nkilib();
 
 namespace {
 
 using FamilyFn = const Family* (*)();
 const FamilyFn kFamilyFns[] = {
-    family_rmsnorm,     family_rmsnorm_weighted, family_layernorm, family_softmax,
-    family_rope,        family_rope_llama3,      family_fused_adam, family_cumsum,
-    family_cumsum_probs,
+    family_rmsnorm,        family_rmsnorm_weighted,   family_layernorm,     family_softmax,
+    family_rope,           family_rope_llama3,        family_fused_adam,    family_cumsum,
+    family_cumsum_probs,   family_matmul,             family_matmul_std002, family_rmsnorm_matmul,
+    family_rmsnorm_matmul_eps, family_silu_mlp,  family_attention_causal, family_attention_nkilib,
 };
 constexpr int kNumFamilies = sizeof(kFamilyFns) / sizeof(kFamilyFns[0]);
 

@@ -1,0 +1,708 @@
+// bf16 MFMA GEMM family: matmul, matmul_std002, rmsnorm_matmul (sum form),
+// rmsnorm_matmul_eps, and the two-stage silu_mlp.
+//
+//   matmul               C = A @ B                         kernels/matmul/kernel.py:7-8
+//   rmsnorm_matmul       C = diag(1/sqrt(sum_k A^2)) (A @ B)  kernels/rmsnorm_matmul/kernel.py:7-16
+//   rmsnorm_matmul_eps   C = diag(rsqrt(mean_k A^2 + 1e-6)) (A @ B)
+//   silu_mlp             H = silu(X @ W1) * (X @ W2);  C = H @ W3  kernels/silu_mlp/kernel.py:7-14
+// A is [M, K] row-major (K contiguous), B is [K, N] row-major (N contiguous),
+// C is [M, N] bf16; accumulation is fp32.
+//
+// Schedule (hw variant 0): a workgroup of 4 waves (2 x 2) owns a BM x BN
+// output tile and a K range of 64*TK. Per 64-deep K step it loads the A tile
+// (16-byte vectors along K) and the B tile (16-byte vectors along N) into
+// registers, stores A to LDS as is and B transposed (each thread turns KR
+// rows x 8 columns into 8 rows of KR k-values), so both MFMA operands are
+// read from LDS as 16-byte k-runs. The next step's global loads are issued
+// before the current step's MFMAs (v_mfma_f32_32x32x16_bf16), so HBM latency
+// hides behind the matrix cores; LDS is double-buffered.
+// The RMSNorm row scale needs sum_k A^2: each thread accumulates the squares
+// of the A vectors it already holds, so A is read once.
+// Split K (K range < K): each workgroup writes its fp32 partial tile (and its
+// rows' partial sums of squares) to the workspace, bumps a per-tile counter,
+// and the last of the S workgroups of a tile sums the S partials in split
+// order (deterministic), applies the epilogue, writes C and re-arms the
+// counter to zero. No workgroup ever waits on another.
+// Workgroups are numbered so that the ones sharing a K range land on the same
+// XCD (blocks are dealt round-robin over the 8 XCDs), keeping that range of A
+// and B in one L2.
+//
+// Tile arguments: TILES_IN_BLOCK_M = BM/32, TILES_IN_BLOCK_N = BN/32,
+//                 TILES_IN_BLOCK_K = K range per workgroup / 64
+//                 (silu_mlp: TILES_IN_BLOCK_P = BN/32 of its second GEMM).
+#include <atomic>
+
+#include "common.hpp"
+#include "registry.hpp"
+
+namespace axon {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BK = 64;
+constexpr int LDK = BK + 8;  // LDS row pitch in elements (144 B; keeps 16 B alignment)
+constexpr int kThreads = 256;
+constexpr int kXcds = 8;
+
+enum Epi { kPlain = 0, kRmsSum = 1, kRmsEps = 2, kSiluMul = 3 };
+
+struct GemmArgs {
+  const void* A;        // [M, K] bf16, or fp32 when A_F32
+  const bf16* B;        // [K, N]
+  const bf16* B2;       // [K, N] second operand (kSiluMul)
+  void* C;              // [M, N] bf16, or fp32 H when kSiluMul
+  float* partial;       // [S][M][N] fp32 (x2 for kSiluMul)
+  float* rowsq;         // [S][NT][M] fp32
+  unsigned* counters;   // [MT * NT]
+  int M, N, K;
+  int kchunk;           // K range per workgroup
+  int S, MT, NT;
+  float eps;
+};
+
+__device__ __forceinline__ float silu(float a) { return a / (1.f + __expf(-a)); }
+
+template <int BM, int BN, int EPI, bool A_F32>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
+  constexpr bool DUAL = EPI == kSiluMul;
+  constexpr int WM = BM / 2, WN = BN / 2;  // per-wave tile
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int AV = BM * BK / 8 / kThreads;  // A vectors per thread (8 k-values each)
+  constexpr int KR = BN / 32;                 // B rows per thread block (k)
+  constexpr int NA = A_F32 ? 2 : 1;           // hi/lo planes for an fp32 A
+  constexpr int NB = DUAL ? 2 : 1;
+  static_assert(AV >= 1 && KR >= 2 && KR <= 8, "tile shape");
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* As = reinterpret_cast<bf16*>(smem);                 // [2][NA][BM][LDK]
+  bf16* Bs = As + 2 * NA * BM * LDK;                        // [2][NB][BN][LDK]
+  __shared__ unsigned ticket_lds;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // XCD-aware numbering: blocks b and b+8 run on the same XCD; give each XCD
+  // a contiguous run of (split, tile) units in split-major order.
+  const int G = g.S * g.MT * g.NT;
+  int unit = blockIdx.x;
+  if (G % kXcds == 0) unit = (blockIdx.x % kXcds) * (G / kXcds) + blockIdx.x / kXcds;
+  const int z = unit / (g.MT * g.NT);
+  const int tile = unit - z * g.MT * g.NT;
+  const int mt = tile / g.NT, nt = tile - mt * g.NT;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int kbeg = z * g.kchunk;
+  const int kend = min(g.K, kbeg + g.kchunk);
+
+  // Global-load assignment.
+  // A: vector v = tid + j*256 -> row v/8, k-chunk v%8.
+  // B: thread -> (k block kb, column chunk nc): rows kb*KR..+KR, columns nc*8..+8.
+  const int b_nc = tid % (BN / 8);
+  const int b_kb = tid / (BN / 8);
+
+  float a_reg[AV][8];
+  bf16 b_reg[NB][KR][8];
+  float sq[AV];
+#pragma unroll
+  for (int j = 0; j < AV; ++j) sq[j] = 0.f;
+
+  auto load_global = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < AV; ++j) {
+      const int v = tid + j * kThreads;
+      const int r = v >> 3, kc = (v & 7) * 8;
+      const int gm = m0 + r, gk = k0 + kc;
+      const bool in = gm < g.M && gk < kend;
+      if constexpr (A_F32) {
+        const float* src = static_cast<const float*>(g.A) + static_cast<int64_t>(gm) * g.K + gk;
+        if (in) {
+          const Vec<float> lo = load_vec(src), hi = load_vec(src + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            a_reg[j][e] = lo.v[e];
+            a_reg[j][4 + e] = hi.v[e];
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a_reg[j][e] = 0.f;
+        }
+      } else {
+        const bf16* src = static_cast<const bf16*>(g.A) + static_cast<int64_t>(gm) * g.K + gk;
+        if (in) {
+          const Vec<bf16> t = load_vec(src);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a_reg[j][e] = to_f32(t.v[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a_reg[j][e] = 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const bf16* Bq = q == 0 ? g.B : g.B2;
+#pragma unroll
+      for (int r = 0; r < KR; ++r) {
+        const int gk = k0 + b_kb * KR + r;
+        const int gn = n0 + b_nc * 8;
+        if (gk < kend && gn < g.N) {
+          const Vec<bf16> t = load_vec(Bq + static_cast<int64_t>(gk) * g.N + gn);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) b_reg[q][r][e] = t.v[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) b_reg[q][r][e] = static_cast<bf16>(0.f);
+        }
+      }
+    }
+  };
+
+  auto store_lds = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < AV; ++j) {
+      const int v = tid + j * kThreads;
+      const int r = v >> 3, kc = (v & 7) * 8;
+      Vec<bf16> hi;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hi.v[e] = static_cast<bf16>(a_reg[j][e]);
+      store_vec(As + ((buf * NA + 0) * BM + r) * LDK + kc, hi);
+      if constexpr (A_F32) {
+        Vec<bf16> lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          lo.v[e] = static_cast<bf16>(a_reg[j][e] - static_cast<float>(hi.v[e]));
+        store_vec(As + ((buf * NA + 1) * BM + r) * LDK + kc, lo);
+      }
+      if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sq[j] += a_reg[j][e] * a_reg[j][e];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      bf16* dst = Bs + ((buf * NB + q) * BN + b_nc * 8) * LDK + b_kb * KR;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        // KR k-values of column b_nc*8 + i.
+        if constexpr (KR == 8) {
+          Vec<bf16> t;
+#pragma unroll
+          for (int r = 0; r < 8; ++r) t.v[r] = b_reg[q][r][i];
+          store_vec(dst + i * LDK, t);
+        } else if constexpr (KR == 4) {
+          typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+          bf16x4 t;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) t[r] = b_reg[q][r][i];
+          *reinterpret_cast<bf16x4*>(dst + i * LDK) = t;
+        } else {
+          typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+          bf16x2 t;
+          t[0] = b_reg[q][0][i];
+          t[1] = b_reg[q][1][i];
+          *reinterpret_cast<bf16x2*>(dst + i * LDK) = t;
+        }
+      }
+    }
+  };
+
+  floatx16 acc[NB][TM][TN];
+#pragma unroll
+  for (int q = 0; q < NB; ++q)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[q][i][j][e] = 0.f;
+
+  const int nsteps = (kend - kbeg + BK - 1) / BK;
+  if (nsteps > 0) {
+    load_global(kbeg);
+    store_lds(0);
+  }
+  __syncthreads();
+  for (int s = 0; s < nsteps; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nsteps) load_global(kbeg + (s + 1) * BK);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int kof = kk * 16 + (lane >> 5) * 8;
+      bf16x8 af[NA][TM];
+#pragma unroll
+      for (int p = 0; p < NA; ++p)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          af[p][i] = *reinterpret_cast<const bf16x8*>(
+              As + ((buf * NA + p) * BM + wm * WM + i * 32 + (lane & 31)) * LDK + kof);
+#pragma unroll
+      for (int q = 0; q < NB; ++q) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(
+              Bs + ((buf * NB + q) * BN + wn * WN + j * 32 + (lane & 31)) * LDK + kof);
+#pragma unroll
+          for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int p = 0; p < NA; ++p)
+              acc[q][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[p][i], bfr, acc[q][i][j], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (s + 1 < nsteps) store_lds(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- row sums of squares (RMSNorm epilogues) ---------------------------
+  float* rs_lds = reinterpret_cast<float*>(smem);  // [BM], reuses the A buffers
+  if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
+#pragma unroll
+    for (int j = 0; j < AV; ++j) {
+      float v = sq[j];
+      v += __shfl_xor(v, 1, kWave);
+      v += __shfl_xor(v, 2, kWave);
+      v += __shfl_xor(v, 4, kWave);
+      sq[j] = v;  // row (tid + j*256)/8, identical across its 8 threads
+    }
+    if (g.S == 1) {
+#pragma unroll
+      for (int j = 0; j < AV; ++j)
+        if ((tid & 7) == 0) rs_lds[(tid + j * kThreads) >> 3] = sq[j];
+      __syncthreads();
+    } else {
+#pragma unroll
+      for (int j = 0; j < AV; ++j) {
+        const int r = (tid + j * kThreads) >> 3;
+        if ((tid & 7) == 0 && m0 + r < g.M)
+          g.rowsq[(static_cast<int64_t>(z) * g.NT + nt) * g.M + m0 + r] = sq[j];
+      }
+    }
+  }
+
+  // Output coordinates of accumulator element e of MFMA tile (i, j):
+  // row = 8*(e/4) + 4*(lane/32) + e%4, column = lane%32.
+  auto row_of = [&](int i, int e) { return wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); };
+  auto col_of = [&](int j) { return wn * WN + j * 32 + (lane & 31); };
+
+  auto scale_of = [&](float sumsq) -> float {
+    if constexpr (EPI == kRmsSum) return 1.f / sqrtf(sumsq);
+    else if constexpr (EPI == kRmsEps) return 1.f / sqrtf(sumsq / static_cast<float>(g.K) + g.eps);
+    else return 1.f;
+  };
+
+  auto write_out = [&](int gm, int gn, float v0, float v1) {
+    if constexpr (EPI == kSiluMul) {
+      static_cast<float*>(g.C)[static_cast<int64_t>(gm) * g.N + gn] = silu(v0) * v1;
+    } else {
+      (void)v1;
+      static_cast<bf16*>(g.C)[static_cast<int64_t>(gm) * g.N + gn] = static_cast<bf16>(v0);
+    }
+  };
+
+  if (g.S == 1) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = row_of(i, e);
+        const int gm = m0 + r;
+        if (gm >= g.M) continue;
+        float sc = 1.f;
+        if constexpr (EPI == kRmsSum || EPI == kRmsEps) sc = scale_of(rs_lds[r]);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int gn = n0 + col_of(j);
+          if (gn >= g.N) continue;
+          write_out(gm, gn, acc[0][i][j][e] * sc, acc[NB - 1][i][j][e]);
+        }
+      }
+    return;
+  }
+
+  // ---- split K: publish the partial, the last arriver reduces ------------
+  const int64_t MN = static_cast<int64_t>(g.M) * g.N;
+#pragma unroll
+  for (int q = 0; q < NB; ++q)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int gm = m0 + row_of(i, e);
+        if (gm >= g.M) continue;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int gn = n0 + col_of(j);
+          if (gn < g.N) g.partial[(static_cast<int64_t>(q) * g.S + z) * MN + static_cast<int64_t>(gm) * g.N + gn] = acc[q][i][j][e];
+        }
+      }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) ticket_lds = atomicAdd(&g.counters[tile], 1u);
+  __syncthreads();
+  if (ticket_lds != static_cast<unsigned>(g.S - 1)) return;
+  __threadfence();
+  if (tid == 0) atomicExch(&g.counters[tile], 0u);  // re-arm for the next launch
+
+  if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
+    for (int r = tid; r < BM; r += kThreads) {
+      float t = 0.f;
+      if (m0 + r < g.M)
+        for (int zz = 0; zz < g.S; ++zz)
+          t += __builtin_nontemporal_load(&g.rowsq[(static_cast<int64_t>(zz) * g.NT + nt) * g.M + m0 + r]);
+      rs_lds[r] = t;
+    }
+    __syncthreads();
+  }
+  // Coalesced reduction over the tile: thread -> column, loop over rows.
+  for (int idx = tid; idx < BM * BN; idx += kThreads) {
+    const int r = idx / BN, c = idx - r * BN;
+    const int gm = m0 + r, gn = n0 + c;
+    if (gm >= g.M || gn >= g.N) continue;
+    const int64_t off = static_cast<int64_t>(gm) * g.N + gn;
+    float v[NB];
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      float t = 0.f;
+      for (int zz = 0; zz < g.S; ++zz)
+        t += __builtin_nontemporal_load(&g.partial[(static_cast<int64_t>(q) * g.S + zz) * MN + off]);
+      v[q] = t;
+    }
+    float sc = 1.f;
+    if constexpr (EPI == kRmsSum || EPI == kRmsEps) sc = scale_of(rs_lds[r]);
+    write_out(gm, gn, v[0] * sc, v[NB - 1]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+const char* const kTileArgs3[] = {"TILES_IN_BLOCK_M", "TILES_IN_BLOCK_N", "TILES_IN_BLOCK_K"};
+const char* const kTileArgs4[] = {"TILES_IN_BLOCK_M", "TILES_IN_BLOCK_N", "TILES_IN_BLOCK_K",
+                                  "TILES_IN_BLOCK_P"};
+
+struct Plan {
+  int BM, BN, kchunk, S, MT, NT;
+};
+
+Plan plan_of(int M, int N, int K, int tm, int tn, int tk) {
+  Plan p;
+  p.BM = 32 * tm;
+  p.BN = 32 * tn;
+  p.kchunk = BK * tk;
+  if (p.kchunk > K) p.kchunk = ((K + BK - 1) / BK) * BK;
+  p.S = K > 0 ? (K + p.kchunk - 1) / p.kchunk : 1;
+  p.MT = (M + p.BM - 1) / p.BM;
+  p.NT = (N + p.BN - 1) / p.BN;
+  return p;
+}
+
+bool tile_ok(int tm, int tn) {
+  // (BM, BN) instantiations: BM in {64, 128, 256}, BN in {64, 128, 256}.
+  return (tm == 2 || tm == 4 || tm == 8) && (tn == 2 || tn == 4 || tn == 8);
+}
+
+size_t lds_bytes(int BM, int BN, int na, int nb) {
+  return static_cast<size_t>(2) * (na * BM + nb * BN) * LDK * sizeof(bf16);
+}
+
+// Dynamic LDS available to one workgroup (160 KiB on gfx950, less the small
+// static allocation of the kernel).
+constexpr size_t kMaxLds = 160 * 1024 - 256;
+
+int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, std::string* why) {
+  if (M < 0 || N < 0 || K < 0 || M > (1 << 30) || N > (1 << 30) || K > (1 << 30)) {
+    *why = "dimension out of range";
+    return AXON_EINVAL;
+  }
+  if (N % 8 != 0 || K % 8 != 0) {
+    *why = "n and k must be multiples of 8 (16-byte rows)";
+    return AXON_EINVAL;
+  }
+  if (!tile_ok(tm, tn)) {
+    *why = "TILES_IN_BLOCK_M/N must each be 2, 4 or 8 (tiles of 64, 128 or 256)";
+    return AXON_EINVAL;
+  }
+  if (tm * tn > 32) {
+    *why = "a 256 x 256 tile exceeds the register budget of 4 waves";
+    return AXON_EINVAL;
+  }
+  if (!is_pow2_in(tk, 1, 1 << 20)) {
+    *why = "TILES_IN_BLOCK_K must be a positive power of two";
+    return AXON_EINVAL;
+  }
+  const Plan p = plan_of(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), tm, tn, tk);
+  if (static_cast<int64_t>(p.S) * p.MT * p.NT > (1LL << 31) - 1) {
+    *why = "grid too large";
+    return AXON_EINVAL;
+  }
+  return AXON_OK;
+}
+
+size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+// Split-K workspace layout: [tile counters, 256-byte aligned][partials][row
+// sums of squares]. The counter region always sits at the start, so GEMMs
+// run back to back on one workspace (silu_mlp's two stages) share it, and
+// each leaves its counters at zero for the next.
+size_t counter_bytes(const Plan& p) {
+  return p.S > 1 ? align256(static_cast<size_t>(p.MT) * p.NT * sizeof(unsigned)) : 0;
+}
+
+size_t data_bytes(const Plan& p, int M, int N, int nb) {
+  if (p.S <= 1) return 0;
+  return static_cast<size_t>(nb) * p.S * M * N * sizeof(float) +  // partials
+         static_cast<size_t>(p.S) * p.NT * M * sizeof(float);     // row sums of squares
+}
+
+size_t gemm_workspace(int M, int N, int K, int tm, int tn, int tk, int nb) {
+  const Plan p = plan_of(M, N, K, tm, tn, tk);
+  return counter_bytes(p) + data_bytes(p, M, N, nb);
+}
+
+template <int BM, int BN, int EPI, bool AF>
+void launch_tile(const GemmArgs& g, hipStream_t st) {
+  constexpr int na = AF ? 2 : 1, nb = EPI == kSiluMul ? 2 : 1;
+  const size_t lds = lds_bytes(BM, BN, na, nb);
+  auto fn = gemm_kernel<BM, BN, EPI, AF>;
+  // Raising the dynamic LDS limit is idempotent, so a race between threads
+  // doing it for the first time is harmless.
+  static std::atomic<bool> configured{false};
+  if (!configured.load(std::memory_order_acquire)) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                        static_cast<int>(lds));
+    configured.store(true, std::memory_order_release);
+  }
+  const unsigned blocks = static_cast<unsigned>(g.S * g.MT * g.NT);
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(kThreads), lds, st, g);
+}
+
+template <int EPI, bool AF>
+int dispatch(int BM, int BN, const GemmArgs& g, hipStream_t st) {
+#define AXON_GEMM_CASE(bm, bn) \
+  if (BM == bm && BN == bn) { launch_tile<bm, bn, EPI, AF>(g, st); return launch_status("gemm_kernel"); }
+  AXON_GEMM_CASE(64, 64)
+  AXON_GEMM_CASE(64, 128)
+  AXON_GEMM_CASE(64, 256)
+  AXON_GEMM_CASE(128, 64)
+  AXON_GEMM_CASE(128, 128)
+  AXON_GEMM_CASE(128, 256)
+  AXON_GEMM_CASE(256, 64)
+  AXON_GEMM_CASE(256, 128)
+#undef AXON_GEMM_CASE
+  set_error("no GEMM instantiation for this tile");
+  return AXON_EINVAL;
+}
+
+// Fills a GemmArgs for C = A @ B (+ epilogue). `ctr` is the counter region,
+// `data` the partial/row-sum region (both unused when the plan has S == 1).
+GemmArgs make_args(const void* A, const bf16* B, const bf16* B2, void* C, int M, int N, int K,
+                   const Plan& p, void* ctr, void* data, int nb, float eps) {
+  GemmArgs g{};
+  g.A = A;
+  g.B = B;
+  g.B2 = B2;
+  g.C = C;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.kchunk = p.kchunk;
+  g.S = p.S;
+  g.MT = p.MT;
+  g.NT = p.NT;
+  g.eps = eps;
+  if (p.S > 1) {
+    char* w = static_cast<char*>(data);
+    g.partial = reinterpret_cast<float*>(w);
+    g.rowsq = reinterpret_cast<float*>(w + static_cast<size_t>(nb) * p.S * M * N * sizeof(float));
+    g.counters = static_cast<unsigned*>(ctr);
+  }
+  return g;
+}
+
+// ---- matmul-like families (dims m, n, k; inputs x[m,k], w[k,n]) ----------
+template <int EPI>
+int check_mm(const Call& c, std::string* why) {
+  if (c.n_tiles != 3 || c.n_dims != 3 || c.n_dtypes != 2) {
+    *why = "expected 3 tiles, 3 dims (m, n, k) and 2 dtypes";
+    return AXON_EARG;
+  }
+  if (c.dtype(0) != AXON_BF16 || c.dtype(1) != AXON_BF16) {
+    *why = "bf16 inputs only";
+    return AXON_EDTYPE;
+  }
+  return check_gemm_shape(c.dim(0), c.dim(1), c.dim(2), c.tile(0), c.tile(1), c.tile(2), why);
+}
+
+int manifest_mm(int, const int64_t* dims, int, Constraint* out, int cap) {
+  if (cap < 3) return 0;
+  const int64_t m = dims[0] > 0 ? dims[0] : 1, n = dims[1] > 0 ? dims[1] : 1;
+  const int64_t k = dims[2] > 0 ? dims[2] : 1;
+  // Tiles of 64..256 that fit the extent (a 64-wide tile is always allowed).
+  out[0] = {"TILES_IN_BLOCK_M", m < 256 ? (m < 64 ? 64 : m) : 256, 32, false};
+  out[1] = {"TILES_IN_BLOCK_N", n < 256 ? (n < 64 ? 64 : n) : 256, 32, false};
+  out[2] = {"TILES_IN_BLOCK_K", k < 64 ? 64 : k, 64, true};
+  return 3;
+}
+
+template <int EPI>
+size_t workspace_mm(const Call& c) {
+  return gemm_workspace(static_cast<int>(c.dim(0)), static_cast<int>(c.dim(1)),
+                        static_cast<int>(c.dim(2)), c.tile(0), c.tile(1), c.tile(2), 1);
+}
+
+void outputs_mm(const int64_t* dims, const int32_t*, OutDesc* out) {
+  out[0] = {2, {dims[0], dims[1]}, AXON_BF16};
+}
+
+template <int EPI>
+int launch_mm(const Call& c, const void* const* in, void* const* out, void* ws, hipStream_t st) {
+  const int M = static_cast<int>(c.dim(0)), N = static_cast<int>(c.dim(1)), K = static_cast<int>(c.dim(2));
+  if (M == 0 || N == 0) return AXON_OK;
+  if (!aligned16(in[0]) || !aligned16(in[1]) || !aligned16(out[0])) {
+    set_error("GEMM buffers must be 16-byte aligned");
+    return AXON_EARG;
+  }
+  const Plan p = plan_of(M, N, K, c.tile(0), c.tile(1), c.tile(2));
+  void* data = static_cast<char*>(ws) + counter_bytes(p);
+  const GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[1]), nullptr, out[0], M, N, K, p, ws,
+                               data, 1, 1e-6f);
+  return dispatch<EPI, false>(p.BM, p.BN, g, st);
+}
+
+const char* summary_mm(int) {
+  return "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, LDS double buffer with B transposed on store, "
+         "split-K with last-arriver reduction, XCD-grouped K ranges, fused row-scale epilogue";
+}
+
+// ---- silu_mlp (dims m, n, k, p; x[m,k], w1[k,n], w2[k,n], w3[n,p]) --------
+int check_mlp(const Call& c, std::string* why) {
+  if (c.n_tiles != 4 || c.n_dims != 4 || c.n_dtypes != 4) {
+    *why = "expected 4 tiles, 4 dims (m, n, k, p) and 4 dtypes";
+    return AXON_EARG;
+  }
+  for (int i = 0; i < 4; ++i)
+    if (c.dtype(i) != AXON_BF16) {
+      *why = "bf16 inputs only";
+      return AXON_EDTYPE;
+    }
+  const int64_t m = c.dim(0), n = c.dim(1), k = c.dim(2), p = c.dim(3);
+  // Stage 1 (k-contraction) uses M/N/K tiles; stage 2 (n-contraction) uses
+  // M/P tiles with the same K range.
+  int rc = check_gemm_shape(m, n, k, c.tile(0), c.tile(1), c.tile(2), why);
+  if (rc != AXON_OK) return rc;
+  if (c.tile(0) * c.tile(1) > 16) {
+    *why = "stage 1 keeps two accumulator sets: BM x BN at most 128 x 128";
+    return AXON_EINVAL;
+  }
+  if (lds_bytes(32 * c.tile(0), 32 * c.tile(1), 1, 2) > kMaxLds ||
+      lds_bytes(32 * c.tile(0), 32 * c.tile(3), 2, 1) > kMaxLds) {
+    *why = "tile needs more LDS than a workgroup may hold (160 KiB)";
+    return AXON_EINVAL;
+  }
+  rc = check_gemm_shape(m, p, n, c.tile(0), c.tile(3), c.tile(2), why);
+  if (rc != AXON_OK) return rc;
+  if (c.tile(0) * c.tile(3) > 16) {
+    *why = "stage 2 splits its fp32 operand into two bf16 planes: BM x BP at most 128 x 128";
+    return AXON_EINVAL;
+  }
+  return AXON_OK;
+}
+
+int manifest_mlp(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
+  if (cap < 4) return 0;
+  const int64_t mnk[3] = {dims[0], dims[1], dims[2]};
+  manifest_mm(v, mnk, dt, out, cap);
+  const int64_t p = dims[3] > 0 ? dims[3] : 1;
+  out[3] = {"TILES_IN_BLOCK_P", p < 256 ? (p < 64 ? 64 : p) : 256, 32, false};
+  return 4;
+}
+
+// silu_mlp workspace: [counters, sized for the larger stage][H fp32 m x n]
+// [split-K data of whichever stage needs more].
+struct MlpLayout {
+  Plan p1, p2;
+  size_t ctr, h, data;
+};
+
+MlpLayout mlp_layout(const Call& c) {
+  const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1));
+  const int k = static_cast<int>(c.dim(2)), p = static_cast<int>(c.dim(3));
+  MlpLayout L;
+  L.p1 = plan_of(m, n, k, c.tile(0), c.tile(1), c.tile(2));
+  L.p2 = plan_of(m, p, n, c.tile(0), c.tile(3), c.tile(2));
+  const size_t c1 = counter_bytes(L.p1), c2 = counter_bytes(L.p2);
+  L.ctr = c1 > c2 ? c1 : c2;
+  L.h = align256(static_cast<size_t>(m) * n * sizeof(float));
+  const size_t d1 = data_bytes(L.p1, m, n, 2), d2 = data_bytes(L.p2, m, p, 1);
+  L.data = d1 > d2 ? d1 : d2;
+  return L;
+}
+
+size_t workspace_mlp(const Call& c) {
+  const MlpLayout L = mlp_layout(c);
+  return L.ctr + L.h + L.data;
+}
+
+void outputs_mlp(const int64_t* dims, const int32_t*, OutDesc* out) {
+  out[0] = {2, {dims[0], dims[3]}, AXON_BF16};
+}
+
+int launch_mlp(const Call& c, const void* const* in, void* const* out, void* ws, hipStream_t st) {
+  const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1));
+  const int k = static_cast<int>(c.dim(2)), p = static_cast<int>(c.dim(3));
+  if (m == 0 || p == 0) return AXON_OK;
+  for (int i = 0; i < 4; ++i)
+    if (!aligned16(in[i])) {
+      set_error("GEMM buffers must be 16-byte aligned");
+      return AXON_EARG;
+    }
+  if (!aligned16(out[0]) || ws == nullptr) {
+    set_error("silu_mlp needs an aligned output and its workspace");
+    return AXON_EARG;
+  }
+  const MlpLayout L = mlp_layout(c);
+  char* base = static_cast<char*>(ws);
+  void* ctr = base;
+  float* H = reinterpret_cast<float*>(base + L.ctr);
+  void* data = base + L.ctr + L.h;
+  const GemmArgs g1 = make_args(in[0], static_cast<const bf16*>(in[1]), static_cast<const bf16*>(in[2]),
+                                H, m, n, k, L.p1, ctr, data, 2, 0.f);
+  int rc = dispatch<kSiluMul, false>(L.p1.BM, L.p1.BN, g1, st);
+  if (rc != AXON_OK) return rc;
+  const GemmArgs g2 = make_args(H, static_cast<const bf16*>(in[3]), nullptr, out[0], m, p, n, L.p2,
+                                ctr, data, 1, 0.f);
+  return dispatch<kPlain, true>(L.p2.BM, L.p2.BN, g2, st);
+}
+
+const char* summary_mlp(int) {
+  return "stage 1: one MFMA pass over x with both w1 and w2 tiles, H = silu(x w1) * (x w2) kept in "
+         "fp32; stage 2: H split into bf16 hi + lo planes (two MFMAs per step) times w3";
+}
+
+}  // namespace
+
+#define AXON_MM_FAMILY(fn_name, spec_name, EPI)                                                \
+  const Family* fn_name() {                                                                  \
+    static const Family f = {spec_name,     1,           2,         1,           3,          \
+                             kTileArgs3,    3,           summary_mm, manifest_mm, check_mm<EPI>, \
+                             workspace_mm<EPI>, outputs_mm, launch_mm<EPI>};                  \
+    return &f;                                                                               \
+  }
+
+AXON_MM_FAMILY(family_matmul, "matmul", kPlain)
+AXON_MM_FAMILY(family_matmul_std002, "matmul_std002", kPlain)
+AXON_MM_FAMILY(family_rmsnorm_matmul, "rmsnorm_matmul", kRmsSum)
+AXON_MM_FAMILY(family_rmsnorm_matmul_eps, "rmsnorm_matmul_eps", kRmsEps)
+#undef AXON_MM_FAMILY
+
+const Family* family_silu_mlp() {
+  static const Family f = {"silu_mlp", 1, 4, 1, 4, kTileArgs4, 4, summary_mlp, manifest_mlp,
+                           check_mlp, workspace_mlp, outputs_mlp, launch_mlp};
+  return &f;
+}
+
+}  // namespace axon

@@ -308,7 +308,9 @@ class Launcher:
                     raise HipLibraryError(f"{kernel}: output {i} must be contiguous {d.shape}")
             self.outputs = list(outputs_)
         ws = workspace_bytes(kernel, self.hw_variant, self.tiles, self.dims, self.dtypes)
-        self.workspace = torch.empty(max(ws, 0), dtype=torch.uint8, device=device) if ws else None
+        # A workspace starts zero-filled (split-K tile counters start at zero;
+        # every launch leaves them at zero again).
+        self.workspace = torch.zeros(ws, dtype=torch.uint8, device=device) if ws else None
         self._pack()
 
     def _pack(self) -> None:

@@ -1,0 +1,30 @@
+"""GPU parity for flash attention (causal multi-head config and the
+single-head k_t-transposed reference form) through the C ABI, against the
+fp32 oracle, at rtol = atol = 1e-2 (the bf16 bar; the reference's own cases
+use 5e-2, eval/sizes.json)."""
+
+import pytest
+import torch
+
+from tests._gpu import check_parity
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+
+
+@pytest.mark.parametrize("sizes", [(1, 2, 256, 128), (2, 3, 200, 128), (1, 1, 33, 128), (1, 1, 1, 128)])
+def test_attention_causal_small(sizes):
+    assert check_parity("attention_causal", sizes, rtol=1e-2, atol=1e-2)
+
+
+def test_attention_causal_config():
+    assert check_parity("attention_causal", (1, 32, 4096, 128), rtol=1e-2, atol=1e-2, budget=3)
+
+
+@pytest.mark.parametrize("sizes", [(1024, 128), (2048, 128), (200, 128)])
+def test_attention_nkilib(sizes):
+    assert check_parity("attention_nkilib", sizes, rtol=1e-2, atol=1e-2, budget=5)
