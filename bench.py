@@ -1,0 +1,259 @@
+"""Benchmark of the HIP kernel set on one MI355X; prints one JSON line.
+
+A "step" is one launch of the kernel under test over one batch of its
+synthetic input. The headline workload is RoPE at the Llama-3-8B shape
+(q[1,4096,32,128] + k[1,4096,8,128] bf16, fp32 cos/sin[4096,128] from
+theta = 500000), whose metric is achieved HBM GB/s. Every other BASELINE
+shape (RMSNorm, cumsum over the vocabulary, the 1024x512x16384 matmul and
+its RMSNorm-fused form, causal attention) is measured the same way and
+reported under "configs", each against its roofline (HBM bytes or MFMA
+FLOPs).
+
+Timing: inputs are resident in HBM before the timed region. Launches rotate
+over enough copies of the input/output set to exceed 1 GiB, so the 256 MB
+Infinity Cache cannot serve a set that was just touched. `--warmup` untimed
+launches, then exactly `--steps` launches between two HIP events recorded on
+the stream the kernels are launched on, bracketed by device syncs; the
+average launch duration is the elapsed time / steps.
+
+CPU baseline: the oracle restatement of the same math, timed on the host
+cores (torch, all affinity cores) on the full headline shape; its output is
+also compared with the GPU output as a last guard.
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--headline-only]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+if str(REPO) not in sys.path:
+    sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, 2.5 PFLOP/s
+ROTATE_BYTES = 1 << 30
+
+METRIC = "achieved HBM GB/s (% peak) per norm/rope/scan; MFMA TFLOP/s for matmul/attn"
+
+# name, sizes, variant, tiles (picked by the tile sweep on MI355X), bound,
+# algorithmic work per launch (bytes for "hbm", FLOPs for "mfma"), label.
+CONFIGS = [
+    dict(
+        spec="rope_llama3", sizes=(1, 4096, 32, 8, 128), variant=0, tiles=(2, 1), bound="hbm",
+        work=88_080_384,
+        label="RoPE Llama-3-8B: q[1,4096,32,128] k[1,4096,8,128] bf16, cos/sin[4096,128] fp32, theta 500000",
+    ),
+    dict(
+        spec="rmsnorm_weighted", sizes=(2048, 4096), variant=0, tiles=(2, 2), bound="hbm",
+        work=33_562_624,
+        label="RMSNorm x[2048,4096] bf16, weight[4096] bf16, eps 1e-6",
+    ),
+    dict(
+        spec="cumsum_probs", sizes=(64, 128256), variant=1, tiles=(8, 1), bound="hbm",
+        work=65_667_072,
+        label="cumsum over vocab: probs[64,128256] fp32 (sorted softmax of N(0,3) logits)",
+    ),
+    dict(
+        spec="matmul_std002", sizes=(1024, 512, 16384), variant=0, tiles=(2, 2, 32), bound="mfma",
+        work=2 * 1024 * 512 * 16384,
+        label="matmul m,n,k = 1024,512,16384 bf16 N(0,0.02), fp32 accumulate",
+    ),
+    dict(
+        spec="rmsnorm_matmul_eps", sizes=(1024, 512, 16384), variant=0, tiles=(2, 2, 32), bound="mfma",
+        work=2 * 1024 * 512 * 16384,
+        label="rmsnorm_matmul m,n,k = 1024,512,16384 bf16, eps 1e-6",
+    ),
+    dict(
+        spec="attention_causal", sizes=(1, 32, 4096, 128), variant=0, tiles=(8, 2, 1, 1), bound="mfma",
+        work=137_438_953_472,
+        label="causal attention Q/K/V [1,32,4096,128] bf16, scale 1/sqrt(128)",
+    ),
+]
+
+
+def load_spec(name: str):
+    from enzyme_amd.cli import _load_spec
+
+    return _load_spec(str(REPO / "kernels" / name))
+
+
+def measure(cfg: dict, steps: int, warmup: int):
+    """Average launch duration (us) over `steps` back-to-back launches that
+    rotate over >= 1 GiB of buffer sets; returns (avg_us, first outputs, host inputs)."""
+    import torch
+
+    from enzyme_amd import hip
+    from enzyme_amd.dtypes import to_torch
+    from enzyme_amd.kernel_spec import SEED
+
+    spec = load_spec(cfg["spec"])
+    dims = dict(zip(spec.dim_vars, cfg["sizes"], strict=True))
+    host = spec.make_inputs(**dims, rng=np.random.default_rng(SEED))
+    dev = [to_torch(a).cuda() for a in host]
+    dvals = [dims[d] for d in spec.dim_vars]
+    first = hip.Launcher(spec.name, cfg["variant"], cfg["tiles"], dvals, dev,
+                         input_shapes=spec.input_shapes(dims))
+    per_set = sum(t.numel() * t.element_size() for t in dev + first.outputs)
+    n_sets = max(1, min(64, math.ceil(ROTATE_BYTES / per_set)))
+    sets = [first] + [
+        hip.Launcher(spec.name, cfg["variant"], cfg["tiles"], dvals, [t.clone() for t in dev])
+        for _ in range(n_sets - 1)
+    ]
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        sets[i % n_sets].launch(stream)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        sets[i % n_sets].launch(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    avg_us = start.elapsed_time(end) * 1e3 / steps
+    outs = [o.float().cpu() for o in first.outputs]
+    return avg_us, outs, host, spec
+
+
+def cpu_baseline(cfg: dict, host, gpu_outs, runs: int = 10):
+    """The oracle on the host cores: (median seconds, threads, max error of
+    the GPU output against it)."""
+    import torch
+
+    import oracle
+    from enzyme_amd.dtypes import to_f32_torch
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    fn = oracle.ORACLE[cfg["spec"]]
+    args = [to_f32_torch(a) for a in host]
+    with torch.no_grad():
+        for _ in range(2):
+            ref = fn(*args)
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            ref = fn(*args)
+            times.append(time.perf_counter() - t0)
+    refs = ref if isinstance(ref, tuple) else (ref,)
+    err = max(float((g - r).abs().max()) for g, r in zip(gpu_outs, refs))
+    ok = all(torch.allclose(g, r, rtol=1e-2, atol=1e-2) for g, r in zip(gpu_outs, refs))
+    return float(np.median(times)), torch.get_num_threads(), err, ok
+
+
+def roofline(cfg: dict, avg_us: float) -> dict:
+    if cfg["bound"] == "hbm":
+        achieved = cfg["work"] / (avg_us * 1e-6) / 1e9
+        peak, unit = HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved = cfg["work"] / (avg_us * 1e-6) / 1e12
+        peak, unit = MFMA_BF16_PEAK_TFLOPS, "TFLOP/s"
+    return {"bound": cfg["bound"], "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4)}
+
+
+def traffic_for(kernel: str):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE and
+    scaled against a copy kernel (profiles/traffic_<spec>.json), or None."""
+    p = REPO / "profiles" / f"traffic_{kernel}.json"
+    if not p.is_file():
+        return None
+    try:
+        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every path here runs "
+            "on one MI355X; how each would shard is described in DESIGN.md)",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a visible GPU", file=sys.stderr)
+        return 2
+
+    head = CONFIGS[0]
+    avg_us, outs, host, _ = measure(head, args.steps, args.warmup)
+    line = {
+        "metric": METRIC,
+        "value": None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(avg_us / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded make_inputs of the spec package, inputs resident in HBM)",
+        "config": {
+            "workload": head["label"],
+            "spec": head["spec"],
+            "sizes": list(head["sizes"]),
+            "hw_variant": head["variant"],
+            "tiles": list(head["tiles"]),
+        },
+    }
+    rf = roofline(head, avg_us)
+    rf["traffic"] = traffic_for(head["spec"])
+    line["value"] = rf["achieved"]
+    line["roofline"] = rf
+    if not args.no_cpu:
+        sec, threads, err, ok = cpu_baseline(head, host, outs)
+        line["cpu_baseline"] = {
+            "value": round(head["work"] / sec / 1e9, 3),
+            "unit": "GB/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": "oracle (fp32 torch restatement of the spec's torch_ref) on the full headline "
+                      f"shape, median of 10 runs after 2 warmups: {sec * 1e3:.2f} ms per pass",
+            "gpu_max_abs_err": err,
+            "gpu_allclose_1e-2": ok,
+        }
+    if not args.headline_only:
+        rows = []
+        for cfg in CONFIGS:
+            steps = max(20, args.steps // (4 if cfg["bound"] == "mfma" else 1))
+            us, o, h, _ = measure(cfg, steps, args.warmup)
+            row = {"spec": cfg["spec"], "label": cfg["label"], "tiles": list(cfg["tiles"]),
+                   "hw_variant": cfg["variant"], "us_per_launch": round(us, 3), **roofline(cfg, us)}
+            if not args.no_cpu:
+                runs = 3 if cfg["spec"] == "attention_causal" else 10
+                sec, threads, err, ok = cpu_baseline(cfg, h, o, runs=runs)
+                row["cpu_ms"] = round(sec * 1e3, 3)
+                row["cpu_cores"] = threads
+                row["gpu_max_abs_err"] = err
+            rows.append(row)
+            print(f"# {cfg['spec']}: {us:.2f} us, {row['achieved']} {row['unit']} "
+                  f"({100 * row['frac']:.1f}% of peak)", file=sys.stderr, flush=True)
+        line["configs"] = rows
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
