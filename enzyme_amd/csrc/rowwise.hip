@@ -217,6 +217,11 @@ int check_rows(const Call& c, std::string* why) {
     *why = "TILES_IN_BLOCK_N (16-byte vectors per lane) must be a power of two in [1, 16]";
     return AXON_EINVAL;
   }
+  const int64_t span = static_cast<int64_t>(kWave) * s.E;
+  if (span * s.V > (c.dim(1) > span ? c.dim(1) : span)) {
+    *why = "TILES_IN_BLOCK_N: one wave's vector tile is longer than the row";
+    return AXON_EINVAL;
+  }
   if (s.Wr > kMaxWaves || s.R * s.Wr > kMaxWaves) {
     *why = "rows x waves-per-row = " + std::to_string(s.R) + " x " + std::to_string(s.Wr) +
            " exceeds 16 waves per workgroup";

@@ -1,0 +1,145 @@
+"""The C ABI of libaxon_hip.so on the host: the library loads without a
+GPU, exports every symbol include/axon_hip.h declares, its registry covers
+every spec package, and the host-only entry points (describe, manifest,
+outputs, check, workspace) answer without touching the HIP runtime."""
+
+import re
+from itertools import product
+
+import pytest
+
+from enzyme_amd import hip
+from enzyme_amd.bench_runner import _compile_one_variant
+from enzyme_amd.emit import variant_module_text
+from tests._specs import KERNELS, REPO, load_spec
+
+HEADER = REPO / "include" / "axon_hip.h"
+SPECS = sorted(p.name for p in KERNELS.iterdir() if (p / "__init__.py").is_file())
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(axon_[a-z_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = declared_symbols()
+    assert names and set(names) == set(hip.EXPORTED_SYMBOLS)
+    lib = hip.lib()
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_registry_covers_every_spec_package():
+    assert sorted(hip.kernel_names()) == SPECS
+    for name in SPECS:
+        spec = load_spec(name)
+        n = hip.variant_count(name)
+        assert n >= 1
+        for v in range(n):
+            d = hip.describe(name, v)
+            assert d["tile_args"] == list(spec.tile_args)
+            assert d["n_inputs"] == len(spec.input_specs)
+            assert d["summary"]
+
+
+def test_unknown_kernel_and_variant():
+    assert hip.variant_count("no_such_kernel") == 0
+    st, why = hip.check("no_such_kernel", 0, [1, 1], [1, 1], [0])
+    assert st == hip.AXON_ENOKERNEL and "no_such_kernel" in why
+    st, why = hip.check("rmsnorm", 7, [1, 1], [1, 1], [0])
+    assert st == hip.AXON_ENOKERNEL
+    st, _ = hip.check("rmsnorm", 0, [1, 1, 1], [1, 1], [0])
+    assert st == hip.AXON_EARG
+    st, _ = hip.check("rmsnorm", 0, [1, 1], [4, 64], [hip.AXON_F16])
+    assert st == hip.AXON_EDTYPE
+
+
+@pytest.mark.parametrize("name", SPECS)
+def test_outputs_match_baseline_shapes(name):
+    """Output descriptors agree with the spec's own baseline_op on small inputs."""
+    import numpy as np
+
+    from enzyme_amd.dtypes import to_f32_numpy
+    from tests._specs import spec_inputs
+
+    small = {"rope_llama3": (1, 8, 2, 1, 128), "attention_causal": (1, 2, 16, 128),
+             "attention_nkilib": (16, 128), "silu_mlp": (16, 16, 16, 8), "fused_adam": (4, 16),
+             "rope": (4, 16), "matmul": (8, 16, 16), "matmul_std002": (8, 16, 16),
+             "rmsnorm_matmul": (8, 16, 16), "rmsnorm_matmul_eps": (8, 16, 16)}
+    spec, dims, host = spec_inputs(name, small.get(name, (4, 64)))
+    codes = [hip.AXON_BF16 if str(getattr(a, "dtype", "")).endswith("bfloat16") else hip.AXON_F32
+             for a in host]
+    outs = hip.outputs(name, [dims[d] for d in spec.dim_vars], codes)
+    ref = spec.baseline_op(*[to_f32_numpy(a) for a in host])
+    ref = ref if isinstance(ref, tuple) else (ref,)
+    assert [o.shape for o in outs] == [tuple(np.shape(r)) for r in ref]
+
+
+def test_manifest_literal_reads_back(tmp_path):
+    from axon.candidate_filter import read_manifest
+
+    spec = load_spec("matmul_std002")
+    text = variant_module_text(spec, {"m": 1024, "n": 512, "k": 16384}, 0, 0, hip.AXON_BF16)
+    p = tmp_path / "m.py"
+    p.write_text(text)
+    cons = read_manifest(p)
+    assert cons == tuple(sorted(hip.manifest("matmul_std002", 0, [1024, 512, 16384], hip.AXON_BF16),
+                                key=lambda c: c.tile_arg))
+    k = {c.tile_arg: c for c in cons}["TILES_IN_BLOCK_K"]
+    assert k.require_divisible and k.tile_size == 64 and k.extent == 16384
+
+
+def test_legal_tiles_are_a_subset_of_the_manifest():
+    """Every tile tuple the library accepts passes the manifest the emitter
+    writes (the filter never hides a legal instantiation)."""
+    from axon.candidate_filter import rejection_reason
+
+    cases = {"rmsnorm": [2048, 4096], "cumsum_probs": [64, 128256], "rope_llama3": [1, 4096, 32, 8, 128],
+             "matmul": [1024, 512, 16384], "attention_causal": [1, 32, 4096, 128]}
+    for name, dims in cases.items():
+        spec = load_spec(name)
+        dt = [hip.AXON_F32] if name == "cumsum_probs" else (
+            [0, 0, 2, 2] if name == "rope_llama3" else [0] * len(spec.input_specs))
+        for v in range(hip.variant_count(name)):
+            cons = hip.manifest(name, v, dims, dt[0])
+            legal = [t for t in product(spec.tile_options, repeat=len(spec.tile_args))
+                     if hip.check(name, v, t, dims, dt)[0] == hip.AXON_OK]
+            assert legal, (name, v)
+            for t in legal:
+                assert rejection_reason(spec.tile_args, t, cons) is None, (name, v, t)
+
+
+def test_compile_worker_plans_legal_and_asserts_illegal(tmp_path):
+    spec = load_spec("rmsnorm")
+    mod = tmp_path / "rmsnorm__v0_t0.py"
+    mod.write_text(variant_module_text(spec, {"m": 2048, "n": 4096}, 0, 0, hip.AXON_BF16))
+    art = tmp_path / "__v0_t0_tiles_2_2" / "kernel.plan.json"
+    key, path, err = _compile_one_variant(
+        (str(mod), "rmsnorm", (2, 2), ((2048, 4096), (0,)), {"TILES_IN_BLOCK_M": 2, "TILES_IN_BLOCK_N": 2},
+         str(art), "gfx950", 1))
+    assert err is None and path == str(art) and art.is_file()
+    import json
+
+    plan = json.loads(art.read_text())
+    assert plan["tiles"] == [2, 2] and plan["dims"] == [2048, 4096] and plan["kernel"] == "rmsnorm"
+    art2 = tmp_path / "__v0_t0_tiles_16_2" / "kernel.plan.json"
+    key, path, err = _compile_one_variant(
+        (str(mod), "rmsnorm", (16, 2), ((2048, 4096), (0,)), {"TILES_IN_BLOCK_M": 16, "TILES_IN_BLOCK_N": 2},
+         str(art2), "gfx950", 1))
+    assert path is None and err == "assert" and not art2.exists()
+
+
+def test_workspace_sizes():
+    assert hip.workspace_bytes("rmsnorm", 0, [1, 2], [2048, 4096], [0]) == 0
+    ws = hip.workspace_bytes("cumsum_probs", 1, [8, 1], [64, 128256], [2])
+    assert ws == 64 * ((128256 + 2047) // 2048) * 8
+    assert hip.workspace_bytes("matmul", 0, [2, 2, 16], [1024, 1024, 1024], [0, 0]) == 0
+    assert hip.workspace_bytes("matmul", 0, [2, 2, 32], [1024, 512, 16384], [0, 0]) > 8 * 1024 * 512 * 4
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(hip, "_lib", None)
+    monkeypatch.setattr(hip, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(hip.HipLibraryError, match="missing"):
+        hip.lib()
