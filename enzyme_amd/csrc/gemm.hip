@@ -28,9 +28,10 @@
 // and B in one L2.
 //
 // Tile arguments: TILES_IN_BLOCK_M = BM/32, TILES_IN_BLOCK_N = BN/32,
-//                 TILES_IN_BLOCK_K = K range per workgroup / 64
+//                 TILES_IN_BLOCK_K = K range per workgroup / 256
 //                 (silu_mlp: TILES_IN_BLOCK_P = BN/32 of its second GEMM).
 #include <atomic>
+#include <type_traits>
 
 #include "common.hpp"
 #include "registry.hpp"
@@ -42,6 +43,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BK = 64;
+constexpr int kKUnit = 256;  // TILES_IN_BLOCK_K counts K in units of 256
 constexpr int LDK = BK + 8;  // LDS row pitch in elements (144 B; keeps 16 B alignment)
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
@@ -103,8 +105,16 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   const int b_nc = tid % (BN / 8);
   const int b_kb = tid / (BN / 8);
 
-  float a_reg[AV][8];
-  bf16 b_reg[NB][KR][8];
+  // Global loads are unconditional from clamped (always in-range)
+  // addresses, so the compiler issues them back to back and only waits for
+  // them when the LDS store needs the data, after the current step's MFMAs;
+  // out-of-range elements are zeroed at store time.
+  using ARaw = typename std::conditional<A_F32, Vec<float>, Vec<bf16>>::type;
+  constexpr int AW = A_F32 ? 2 : 1;  // 16-byte loads per 8 A values
+  ARaw a_raw[AV][AW];
+  bool a_ok[AV];
+  Vec<bf16> b_raw[NB][KR];
+  bool b_ok[KR];
   float sq[AV];
 #pragma unroll
   for (int j = 0; j < AV; ++j) sq[j] = 0.f;
@@ -115,48 +125,24 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
       const int v = tid + j * kThreads;
       const int r = v >> 3, kc = (v & 7) * 8;
       const int gm = m0 + r, gk = k0 + kc;
-      const bool in = gm < g.M && gk < kend;
+      a_ok[j] = gm < g.M && gk < kend;
+      const int64_t off = static_cast<int64_t>(min(gm, g.M - 1)) * g.K + min(gk, g.K - 8);
       if constexpr (A_F32) {
-        const float* src = static_cast<const float*>(g.A) + static_cast<int64_t>(gm) * g.K + gk;
-        if (in) {
-          const Vec<float> lo = load_vec(src), hi = load_vec(src + 4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            a_reg[j][e] = lo.v[e];
-            a_reg[j][4 + e] = hi.v[e];
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) a_reg[j][e] = 0.f;
-        }
+        const float* src = static_cast<const float*>(g.A) + off;
+        a_raw[j][0] = load_vec(src);
+        a_raw[j][1] = load_vec(src + 4);
       } else {
-        const bf16* src = static_cast<const bf16*>(g.A) + static_cast<int64_t>(gm) * g.K + gk;
-        if (in) {
-          const Vec<bf16> t = load_vec(src);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) a_reg[j][e] = to_f32(t.v[e]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) a_reg[j][e] = 0.f;
-        }
+        a_raw[j][0] = load_vec(static_cast<const bf16*>(g.A) + off);
       }
     }
 #pragma unroll
-    for (int q = 0; q < NB; ++q) {
-      const bf16* Bq = q == 0 ? g.B : g.B2;
+    for (int r = 0; r < KR; ++r) {
+      const int gk = k0 + b_kb * KR + r;
+      const int gn = n0 + b_nc * 8;
+      b_ok[r] = gk < kend && gn < g.N;
+      const int64_t off = static_cast<int64_t>(min(gk, g.K - 1)) * g.N + min(gn, g.N - 8);
 #pragma unroll
-      for (int r = 0; r < KR; ++r) {
-        const int gk = k0 + b_kb * KR + r;
-        const int gn = n0 + b_nc * 8;
-        if (gk < kend && gn < g.N) {
-          const Vec<bf16> t = load_vec(Bq + static_cast<int64_t>(gk) * g.N + gn);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) b_reg[q][r][e] = t.v[e];
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) b_reg[q][r][e] = static_cast<bf16>(0.f);
-        }
-      }
+      for (int q = 0; q < NB; ++q) b_raw[q][r] = load_vec((q == 0 ? g.B : g.B2) + off);
     }
   };
 
@@ -165,24 +151,45 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     for (int j = 0; j < AV; ++j) {
       const int v = tid + j * kThreads;
       const int r = v >> 3, kc = (v & 7) * 8;
-      Vec<bf16> hi;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) hi.v[e] = static_cast<bf16>(a_reg[j][e]);
-      store_vec(As + ((buf * NA + 0) * BM + r) * LDK + kc, hi);
+      float x[8];
       if constexpr (A_F32) {
-        Vec<bf16> lo;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          lo.v[e] = static_cast<bf16>(a_reg[j][e] - static_cast<float>(hi.v[e]));
+        for (int e = 0; e < 4; ++e) {
+          x[e] = a_ok[j] ? a_raw[j][0].v[e] : 0.f;
+          x[4 + e] = a_ok[j] ? a_raw[j][1].v[e] : 0.f;
+        }
+        Vec<bf16> hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          hi.v[e] = static_cast<bf16>(x[e]);
+          lo.v[e] = static_cast<bf16>(x[e] - static_cast<float>(hi.v[e]));
+        }
+        store_vec(As + ((buf * NA + 0) * BM + r) * LDK + kc, hi);
         store_vec(As + ((buf * NA + 1) * BM + r) * LDK + kc, lo);
+      } else {
+        Vec<bf16> t = a_raw[j][0];
+        if (!a_ok[j]) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) t.v[e] = static_cast<bf16>(0.f);
+        }
+        store_vec(As + ((buf * NA + 0) * BM + r) * LDK + kc, t);
+        if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = to_f32(t.v[e]);
+        }
       }
       if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sq[j] += a_reg[j][e] * a_reg[j][e];
+        for (int e = 0; e < 8; ++e) sq[j] += x[e] * x[e];
       }
     }
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
+      bf16 bv[KR][8];
+#pragma unroll
+      for (int r = 0; r < KR; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bv[r][e] = b_ok[r] ? b_raw[q][r].v[e] : static_cast<bf16>(0.f);
       bf16* dst = Bs + ((buf * NB + q) * BN + b_nc * 8) * LDK + b_kb * KR;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -190,19 +197,19 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         if constexpr (KR == 8) {
           Vec<bf16> t;
 #pragma unroll
-          for (int r = 0; r < 8; ++r) t.v[r] = b_reg[q][r][i];
+          for (int r = 0; r < 8; ++r) t.v[r] = bv[r][i];
           store_vec(dst + i * LDK, t);
         } else if constexpr (KR == 4) {
           typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
           bf16x4 t;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) t[r] = b_reg[q][r][i];
+          for (int r = 0; r < 4; ++r) t[r] = bv[r][i];
           *reinterpret_cast<bf16x4*>(dst + i * LDK) = t;
         } else {
           typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
           bf16x2 t;
-          t[0] = b_reg[q][0][i];
-          t[1] = b_reg[q][1][i];
+          t[0] = bv[0][i];
+          t[1] = bv[1][i];
           *reinterpret_cast<bf16x2*>(dst + i * LDK) = t;
         }
       }
@@ -357,23 +364,40 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
     __syncthreads();
   }
-  // Coalesced reduction over the tile: thread -> column, loop over rows.
-  for (int idx = tid; idx < BM * BN; idx += kThreads) {
+  // Coalesced reduction over the tile: each thread owns 4 consecutive
+  // columns (16-byte loads; N % 8 == 0 keeps a quad inside one row) and
+  // keeps four splits in flight at a time; the sum still runs in split order.
+  for (int idx = tid * 4; idx < BM * BN; idx += kThreads * 4) {
     const int r = idx / BN, c = idx - r * BN;
     const int gm = m0 + r, gn = n0 + c;
     if (gm >= g.M || gn >= g.N) continue;
     const int64_t off = static_cast<int64_t>(gm) * g.N + gn;
-    float v[NB];
+    Vec<float> v[NB];
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
-      float t = 0.f;
-      for (int zz = 0; zz < g.S; ++zz)
-        t += __builtin_nontemporal_load(&g.partial[(static_cast<int64_t>(q) * g.S + zz) * MN + off]);
-      v[q] = t;
+      const float* base = g.partial + static_cast<int64_t>(q) * g.S * MN + off;
+      float t[4] = {0.f, 0.f, 0.f, 0.f};
+      int zz = 0;
+      for (; zz + 4 <= g.S; zz += 4) {
+        const Vec<float> p0 = load_vec(base + (zz + 0) * MN);
+        const Vec<float> p1 = load_vec(base + (zz + 1) * MN);
+        const Vec<float> p2 = load_vec(base + (zz + 2) * MN);
+        const Vec<float> p3 = load_vec(base + (zz + 3) * MN);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = (((t[e] + p0.v[e]) + p1.v[e]) + p2.v[e]) + p3.v[e];
+      }
+      for (; zz < g.S; ++zz) {
+        const Vec<float> p0 = load_vec(base + zz * MN);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] += p0.v[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[q].v[e] = t[e];
     }
     float sc = 1.f;
     if constexpr (EPI == kRmsSum || EPI == kRmsEps) sc = scale_of(rs_lds[r]);
-    write_out(gm, gn, v[0] * sc, v[NB - 1]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) write_out(gm, gn + e, v[0].v[e] * sc, v[NB - 1].v[e]);
   }
 }
 
@@ -392,7 +416,7 @@ Plan plan_of(int M, int N, int K, int tm, int tn, int tk) {
   Plan p;
   p.BM = 32 * tm;
   p.BN = 32 * tn;
-  p.kchunk = BK * tk;
+  p.kchunk = kKUnit * tk;
   if (p.kchunk > K) p.kchunk = ((K + BK - 1) / BK) * BK;
   p.S = K > 0 ? (K + p.kchunk - 1) / p.kchunk : 1;
   p.MT = (M + p.BM - 1) / p.BM;
@@ -544,7 +568,7 @@ int manifest_mm(int, const int64_t* dims, int, Constraint* out, int cap) {
   // Tiles of 64..256 that fit the extent (a 64-wide tile is always allowed).
   out[0] = {"TILES_IN_BLOCK_M", m < 256 ? (m < 64 ? 64 : m) : 256, 32, false};
   out[1] = {"TILES_IN_BLOCK_N", n < 256 ? (n < 64 ? 64 : n) : 256, 32, false};
-  out[2] = {"TILES_IN_BLOCK_K", k < 64 ? 64 : k, 64, true};
+  out[2] = {"TILES_IN_BLOCK_K", k < kKUnit ? kKUnit : k, kKUnit, true};
   return 3;
 }
 

@@ -87,7 +87,7 @@ def test_manifest_literal_reads_back(tmp_path):
     assert cons == tuple(sorted(hip.manifest("matmul_std002", 0, [1024, 512, 16384], hip.AXON_BF16),
                                 key=lambda c: c.tile_arg))
     k = {c.tile_arg: c for c in cons}["TILES_IN_BLOCK_K"]
-    assert k.require_divisible and k.tile_size == 64 and k.extent == 16384
+    assert k.require_divisible and k.tile_size == 256 and k.extent == 16384
 
 
 def test_legal_tiles_are_a_subset_of_the_manifest():
