@@ -134,8 +134,8 @@ def test_workspace_sizes():
     assert hip.workspace_bytes("rmsnorm", 0, [1, 2], [2048, 4096], [0]) == 0
     ws = hip.workspace_bytes("cumsum_probs", 1, [8, 1], [64, 128256], [2])
     assert ws == 64 * ((128256 + 2047) // 2048) * 8
-    assert hip.workspace_bytes("matmul", 0, [2, 2, 16], [1024, 1024, 1024], [0, 0]) == 0
-    assert hip.workspace_bytes("matmul", 0, [2, 2, 32], [1024, 512, 16384], [0, 0]) > 8 * 1024 * 512 * 4
+    assert hip.workspace_bytes("matmul", 0, [2, 2, 4], [1024, 1024, 1024], [0, 0]) == 0
+    assert hip.workspace_bytes("matmul", 0, [2, 2, 8], [1024, 512, 16384], [0, 0]) > 8 * 1024 * 512 * 4
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
