@@ -19,10 +19,9 @@
 // The RMSNorm row scale needs sum_k A^2: each thread accumulates the squares
 // of the A vectors it already holds, so A is read once.
 // Split K (K range < K): each workgroup writes its fp32 partial tile (and its
-// rows' partial sums of squares) to the workspace, bumps a per-tile counter,
-// and the last of the S workgroups of a tile sums the S partials in split
-// order (deterministic), applies the epilogue, writes C and re-arms the
-// counter to zero. No workgroup ever waits on another.
+// rows' partial sums of squares) to the workspace; a second, fully parallel
+// kernel sums the S partials of every output in split order
+// (deterministic), applies the epilogue and writes C.
 // Workgroups are numbered so that the ones sharing a K range land on the same
 // XCD (blocks are dealt round-robin over the 8 XCDs), keeping that range of A
 // and B in one L2.
@@ -57,7 +56,6 @@ struct GemmArgs {
   void* C;              // [M, N] bf16, or fp32 H when kSiluMul
   float* partial;       // [S][M][N] fp32 (x2 for kSiluMul)
   float* rowsq;         // [S][NT][M] fp32
-  unsigned* counters;   // [MT * NT]
   int M, N, K;
   int kchunk;           // K range per workgroup
   int S, MT, NT;
@@ -80,7 +78,6 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   extern __shared__ __align__(16) unsigned char smem[];
   bf16* As = reinterpret_cast<bf16*>(smem);                 // [2][NA][BM][LDK]
   bf16* Bs = As + 2 * NA * BM * LDK;                        // [2][NB][BN][LDK]
-  __shared__ unsigned ticket_lds;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -330,7 +327,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     return;
   }
 
-  // ---- split K: publish the partial, the last arriver reduces ------------
+  // ---- split K: publish the partial; splitk_reduce_kernel finishes -------
   const int64_t MN = static_cast<int64_t>(g.M) * g.N;
 #pragma unroll
   for (int q = 0; q < NB; ++q)
@@ -346,58 +343,60 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
           if (gn < g.N) g.partial[(static_cast<int64_t>(q) * g.S + z) * MN + static_cast<int64_t>(gm) * g.N + gn] = acc[q][i][j][e];
         }
       }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) ticket_lds = atomicAdd(&g.counters[tile], 1u);
-  __syncthreads();
-  if (ticket_lds != static_cast<unsigned>(g.S - 1)) return;
-  __threadfence();
-  if (tid == 0) atomicExch(&g.counters[tile], 0u);  // re-arm for the next launch
+}
 
-  if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
-    for (int r = tid; r < BM; r += kThreads) {
-      float t = 0.f;
-      if (m0 + r < g.M)
-        for (int zz = 0; zz < g.S; ++zz)
-          t += __builtin_nontemporal_load(&g.rowsq[(static_cast<int64_t>(zz) * g.NT + nt) * g.M + m0 + r]);
-      rs_lds[r] = t;
+// Split-K fixup: every thread owns 4 consecutive outputs (16-byte loads;
+// N % 8 == 0 keeps a quad inside one row), sums the S fp32 partials in split
+// order with four splits in flight, applies the epilogue and writes C. The
+// whole grid takes part, so the partials (mostly still in the Infinity
+// Cache) stream at full rate.
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) {
+  constexpr int NB = EPI == kSiluMul ? 2 : 1;
+  const int64_t MN = static_cast<int64_t>(g.M) * g.N;
+  const int64_t idx = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (idx >= MN) return;
+  const int gm = static_cast<int>(idx / g.N), gn = static_cast<int>(idx - static_cast<int64_t>(gm) * g.N);
+  float v[NB][4];
+#pragma unroll
+  for (int q = 0; q < NB; ++q) {
+    const float* base = g.partial + static_cast<int64_t>(q) * g.S * MN + idx;
+    float t[4] = {0.f, 0.f, 0.f, 0.f};
+    int zz = 0;
+    for (; zz + 4 <= g.S; zz += 4) {
+      const Vec<float> p0 = load_vec(base + (zz + 0) * MN);
+      const Vec<float> p1 = load_vec(base + (zz + 1) * MN);
+      const Vec<float> p2 = load_vec(base + (zz + 2) * MN);
+      const Vec<float> p3 = load_vec(base + (zz + 3) * MN);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] = (((t[e] + p0.v[e]) + p1.v[e]) + p2.v[e]) + p3.v[e];
     }
-    __syncthreads();
+    for (; zz < g.S; ++zz) {
+      const Vec<float> p0 = load_vec(base + zz * MN);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] += p0.v[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[q][e] = t[e];
   }
-  // Coalesced reduction over the tile: each thread owns 4 consecutive
-  // columns (16-byte loads; N % 8 == 0 keeps a quad inside one row) and
-  // keeps four splits in flight at a time; the sum still runs in split order.
-  for (int idx = tid * 4; idx < BM * BN; idx += kThreads * 4) {
-    const int r = idx / BN, c = idx - r * BN;
-    const int gm = m0 + r, gn = n0 + c;
-    if (gm >= g.M || gn >= g.N) continue;
-    const int64_t off = static_cast<int64_t>(gm) * g.N + gn;
-    Vec<float> v[NB];
+  float sc = 1.f;
+  if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
+    const int nt = gn / BN;
+    float ss = 0.f;
+    for (int zz = 0; zz < g.S; ++zz) ss += g.rowsq[(static_cast<int64_t>(zz) * g.NT + nt) * g.M + gm];
+    sc = EPI == kRmsSum ? 1.f / sqrtf(ss) : 1.f / sqrtf(ss / static_cast<float>(g.K) + g.eps);
+  }
+  if constexpr (EPI == kSiluMul) {
+    Vec<float> o;
 #pragma unroll
-    for (int q = 0; q < NB; ++q) {
-      const float* base = g.partial + static_cast<int64_t>(q) * g.S * MN + off;
-      float t[4] = {0.f, 0.f, 0.f, 0.f};
-      int zz = 0;
-      for (; zz + 4 <= g.S; zz += 4) {
-        const Vec<float> p0 = load_vec(base + (zz + 0) * MN);
-        const Vec<float> p1 = load_vec(base + (zz + 1) * MN);
-        const Vec<float> p2 = load_vec(base + (zz + 2) * MN);
-        const Vec<float> p3 = load_vec(base + (zz + 3) * MN);
+    for (int e = 0; e < 4; ++e) o.v[e] = silu(v[0][e]) * v[1][e];
+    store_vec(static_cast<float*>(g.C) + idx, o);
+  } else {
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    bf16x4 o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = (((t[e] + p0.v[e]) + p1.v[e]) + p2.v[e]) + p3.v[e];
-      }
-      for (; zz < g.S; ++zz) {
-        const Vec<float> p0 = load_vec(base + zz * MN);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] += p0.v[e];
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[q].v[e] = t[e];
-    }
-    float sc = 1.f;
-    if constexpr (EPI == kRmsSum || EPI == kRmsEps) sc = scale_of(rs_lds[r]);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) write_out(gm, gn + e, v[0].v[e] * sc, v[NB - 1].v[e]);
+    for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(v[0][e] * sc);
+    *reinterpret_cast<bf16x4*>(static_cast<bf16*>(g.C) + idx) = o;
   }
 }
 
@@ -468,14 +467,9 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, st
 
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
-// Split-K workspace layout: [tile counters, 256-byte aligned][partials][row
-// sums of squares]. The counter region always sits at the start, so GEMMs
-// run back to back on one workspace (silu_mlp's two stages) share it, and
-// each leaves its counters at zero for the next.
-size_t counter_bytes(const Plan& p) {
-  return p.S > 1 ? align256(static_cast<size_t>(p.MT) * p.NT * sizeof(unsigned)) : 0;
-}
-
+// Split-K workspace layout: [partials][row sums of squares]; no initial
+// content is required (every element read is written first by the same
+// launch).
 size_t data_bytes(const Plan& p, int M, int N, int nb) {
   if (p.S <= 1) return 0;
   return static_cast<size_t>(nb) * p.S * M * N * sizeof(float) +  // partials
@@ -484,7 +478,7 @@ size_t data_bytes(const Plan& p, int M, int N, int nb) {
 
 size_t gemm_workspace(int M, int N, int K, int tm, int tn, int tk, int nb) {
   const Plan p = plan_of(M, N, K, tm, tn, tk);
-  return counter_bytes(p) + data_bytes(p, M, N, nb);
+  return data_bytes(p, M, N, nb);
 }
 
 template <int BM, int BN, int EPI, bool AF>
@@ -502,6 +496,11 @@ void launch_tile(const GemmArgs& g, hipStream_t st) {
   }
   const unsigned blocks = static_cast<unsigned>(g.S * g.MT * g.NT);
   hipLaunchKernelGGL(fn, dim3(blocks), dim3(kThreads), lds, st, g);
+  if (g.S > 1) {
+    const int64_t quads = static_cast<int64_t>(g.M) * g.N / 4;
+    hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3(static_cast<unsigned>((quads + 255) / 256)),
+                       dim3(256), 0, st, g, BN);
+  }
 }
 
 template <int EPI, bool AF>
@@ -521,10 +520,10 @@ int dispatch(int BM, int BN, const GemmArgs& g, hipStream_t st) {
   return AXON_EINVAL;
 }
 
-// Fills a GemmArgs for C = A @ B (+ epilogue). `ctr` is the counter region,
-// `data` the partial/row-sum region (both unused when the plan has S == 1).
+// Fills a GemmArgs for C = A @ B (+ epilogue); `data` is the partial/row-sum
+// region (unused when the plan has S == 1).
 GemmArgs make_args(const void* A, const bf16* B, const bf16* B2, void* C, int M, int N, int K,
-                   const Plan& p, void* ctr, void* data, int nb, float eps) {
+                   const Plan& p, void* data, int nb, float eps) {
   GemmArgs g{};
   g.A = A;
   g.B = B;
@@ -542,7 +541,6 @@ GemmArgs make_args(const void* A, const bf16* B, const bf16* B2, void* C, int M,
     char* w = static_cast<char*>(data);
     g.partial = reinterpret_cast<float*>(w);
     g.rowsq = reinterpret_cast<float*>(w + static_cast<size_t>(nb) * p.S * M * N * sizeof(float));
-    g.counters = static_cast<unsigned*>(ctr);
   }
   return g;
 }
@@ -591,15 +589,14 @@ int launch_mm(const Call& c, const void* const* in, void* const* out, void* ws, 
     return AXON_EARG;
   }
   const Plan p = plan_of(M, N, K, c.tile(0), c.tile(1), c.tile(2));
-  void* data = static_cast<char*>(ws) + counter_bytes(p);
   const GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[1]), nullptr, out[0], M, N, K, p, ws,
-                               data, 1, 1e-6f);
+                               1, 1e-6f);
   return dispatch<EPI, false>(p.BM, p.BN, g, st);
 }
 
 const char* summary_mm(int) {
   return "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, LDS double buffer with B transposed on store, "
-         "split-K with last-arriver reduction, XCD-grouped K ranges, fused row-scale epilogue";
+         "split-K with a parallel fixup kernel, XCD-grouped K ranges, fused row-scale epilogue";
 }
 
 // ---- silu_mlp (dims m, n, k, p; x[m,k], w1[k,n], w2[k,n], w3[n,p]) --------
@@ -645,21 +642,18 @@ int manifest_mlp(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   return 4;
 }
 
-// silu_mlp workspace: [counters, sized for the larger stage][H fp32 m x n]
-// [split-K data of whichever stage needs more].
 struct MlpLayout {
   Plan p1, p2;
-  size_t ctr, h, data;
+  size_t h, data;
 };
 
+// silu_mlp workspace: [H fp32 m x n][split-K data of whichever stage needs more].
 MlpLayout mlp_layout(const Call& c) {
   const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1));
   const int k = static_cast<int>(c.dim(2)), p = static_cast<int>(c.dim(3));
   MlpLayout L;
   L.p1 = plan_of(m, n, k, c.tile(0), c.tile(1), c.tile(2));
   L.p2 = plan_of(m, p, n, c.tile(0), c.tile(3), c.tile(2));
-  const size_t c1 = counter_bytes(L.p1), c2 = counter_bytes(L.p2);
-  L.ctr = c1 > c2 ? c1 : c2;
   L.h = align256(static_cast<size_t>(m) * n * sizeof(float));
   const size_t d1 = data_bytes(L.p1, m, n, 2), d2 = data_bytes(L.p2, m, p, 1);
   L.data = d1 > d2 ? d1 : d2;
@@ -668,7 +662,7 @@ MlpLayout mlp_layout(const Call& c) {
 
 size_t workspace_mlp(const Call& c) {
   const MlpLayout L = mlp_layout(c);
-  return L.ctr + L.h + L.data;
+  return L.h + L.data;
 }
 
 void outputs_mlp(const int64_t* dims, const int32_t*, OutDesc* out) {
@@ -690,15 +684,14 @@ int launch_mlp(const Call& c, const void* const* in, void* const* out, void* ws,
   }
   const MlpLayout L = mlp_layout(c);
   char* base = static_cast<char*>(ws);
-  void* ctr = base;
-  float* H = reinterpret_cast<float*>(base + L.ctr);
-  void* data = base + L.ctr + L.h;
+  float* H = reinterpret_cast<float*>(base);
+  void* data = base + L.h;
   const GemmArgs g1 = make_args(in[0], static_cast<const bf16*>(in[1]), static_cast<const bf16*>(in[2]),
-                                H, m, n, k, L.p1, ctr, data, 2, 0.f);
+                                H, m, n, k, L.p1, data, 2, 0.f);
   int rc = dispatch<kSiluMul, false>(L.p1.BM, L.p1.BN, g1, st);
   if (rc != AXON_OK) return rc;
   const GemmArgs g2 = make_args(H, static_cast<const bf16*>(in[3]), nullptr, out[0], m, p, n, L.p2,
-                                ctr, data, 1, 0.f);
+                                data, 1, 0.f);
   return dispatch<kPlain, true>(L.p2.BM, L.p2.BN, g2, st);
 }
 
