@@ -99,8 +99,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   // Global-load assignment.
   // A: vector v = tid + j*256 -> row v/8, k-chunk v%8.
   // B: thread -> (k block kb, column chunk nc): rows kb*KR..+KR, columns nc*8..+8.
-  const int b_nc = tid % (BN / 8);
-  const int b_kb = tid / (BN / 8);
+  // kb varies fastest across lanes: the transposed LDS stores of one
+  // instruction then fill contiguous KR-element runs of the same rows (no
+  // bank conflicts), at the price of less coalesced global loads.
+  constexpr int KBN = BK / KR;
+  const int b_kb = tid % KBN;
+  const int b_nc = tid / KBN;
 
   // Global loads are unconditional from clamped (always in-range)
   // addresses, so the compiler issues them back to back and only waits for
