@@ -120,7 +120,9 @@ __global__ __launch_bounds__(256) void copy_kernel(const uint4* __restrict__ src
                                                    uint4* __restrict__ dst, size_t n16) {
   for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16;
        i += static_cast<size_t>(gridDim.x) * blockDim.x)
-    dst[i] = src[i];
+    __builtin_nontemporal_store(
+        __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + i),
+        reinterpret_cast<u32x4*>(dst) + i);
 }
 
 }  // namespace axon

@@ -86,8 +86,8 @@ __global__ __launch_bounds__(1024) void rope_split_kernel(const T* __restrict__ 
     if constexpr (ALIGNED) {
       const int64_t off = vi * E;
       if (off >= len) continue;
-      const Vec<T> a = load_vec(xe + off), b = load_vec(xo + off), c = load_vec(cs + off),
-                   s = load_vec(sn + off);
+      const Vec<T> a = load_vec_nt(xe + off), b = load_vec_nt(xo + off),
+                   c = load_vec_nt(cs + off), s = load_vec_nt(sn + off);
       Vec<T> ra, rb;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
@@ -96,8 +96,8 @@ __global__ __launch_bounds__(1024) void rope_split_kernel(const T* __restrict__ 
         ra.v[e] = from_f32<T>(fa);
         rb.v[e] = from_f32<T>(fb);
       }
-      store_vec(oe + off, ra);
-      store_vec(oo + off, rb);
+      store_vec_nt(oe + off, ra);
+      store_vec_nt(oo + off, rb);
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) {
@@ -129,8 +129,8 @@ __global__ __launch_bounds__(1024) void adam_kernel(
       if (off >= len) continue;
       const int64_t row = off / f;  // f % E == 0: one row per vector
       const float st = to_f32(step[row]), ib = to_f32(ibc[row]), w = to_f32(wd[row]);
-      const Vec<T> pv = load_vec(p + off), gv = load_vec(g + off), mv = load_vec(m + off),
-                   vv = load_vec(v + off);
+      const Vec<T> pv = load_vec_nt(p + off), gv = load_vec_nt(g + off),
+                   mv = load_vec_nt(m + off), vv = load_vec_nt(v + off);
       Vec<T> rp, rm, rv;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
@@ -141,9 +141,9 @@ __global__ __launch_bounds__(1024) void adam_kernel(
         rm.v[e] = from_f32<T>(b);
         rv.v[e] = from_f32<T>(c);
       }
-      store_vec(po + off, rp);
-      store_vec(mo + off, rm);
-      store_vec(vo + off, rv);
+      store_vec_nt(po + off, rp);
+      store_vec_nt(mo + off, rm);
+      store_vec_nt(vo + off, rv);
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) {

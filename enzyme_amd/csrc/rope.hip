@@ -72,8 +72,10 @@ __global__ __launch_bounds__(1024) void rope_tok_kernel(
       src = k + (t * hkv + (h - hq)) * d;
       dst = ko + (t * hkv + (h - hq)) * d;
     }
-    const Vec<T> lo = load_vec(src + j * E);
-    const Vec<T> hi = load_vec(src + half + j * E);
+    // q/k are touched exactly once: non-temporal loads and stores stream
+    // past the caches (cos/sin above stay cached for the other heads).
+    const Vec<T> lo = load_vec_nt(src + j * E);
+    const Vec<T> hi = load_vec_nt(src + half + j * E);
     Vec<T> olo, ohi;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
@@ -82,8 +84,8 @@ __global__ __launch_bounds__(1024) void rope_tok_kernel(
       olo.v[e] = from_f32<T>(a * clo[e] - b * slo[e]);
       ohi.v[e] = from_f32<T>(b * chi[e] + a * shi[e]);
     }
-    store_vec(dst + j * E, olo);
-    store_vec(dst + half + j * E, ohi);
+    store_vec_nt(dst + j * E, olo);
+    store_vec_nt(dst + half + j * E, ohi);
   }
 }
 

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(1024) void rowwise_kernel(const T* __restrict__ x,
     if constexpr (ALIGNED) {
       const bool in = live && off < n;  // n % E == 0, so a vector is all-in or all-out
       if (in) {
-        Vec<T> t = load_vec(xr + off);
+        Vec<T> t = load_vec_nt(xr + off);  // streamed once: bypass cache allocation
 #pragma unroll
         for (int e = 0; e < E; ++e) xv[v][e] = to_f32(t.v[e]);
       } else {
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(1024) void rowwise_kernel(const T* __restrict__ x,
         Vec<T> t;
 #pragma unroll
         for (int e = 0; e < E; ++e) t.v[e] = from_f32<T>(o[e]);
-        store_vec(yr + off, t);
+        store_vec_nt(yr + off, t);
       }
     } else {
 #pragma unroll

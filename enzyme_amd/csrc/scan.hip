@@ -2,24 +2,29 @@
 // "cumsum_probs"; kernels/cumsum/kernel.py:12-13).
 //
 // Accuracy: the fp32 reference (torch.cumsum on the CPU) accumulates in
-// double and rounds each prefix once. Here every chunk is scanned in fp32
-// (a thread's serial run, a wave64 shuffle scan, a scan of wave totals in
-// LDS: at most ~V*E + 6 + 4 additions deep), and the running offset of all
-// earlier chunks is carried in double, so each output is
-// round_fp32(double offset + fp32 local prefix). That keeps the relative
-// error of every prefix within a few fp32 ulps on positive data instead of
-// growing with the row length as a sequential fp32 carry does.
+// double and rounds each prefix once. Here a chunk is scanned in fp32 (each
+// lane's E elements serially, a wave64 shuffle scan per step, a running wave
+// offset across the V steps), while the offsets of earlier waves and chunks
+// are carried in double, so each output is round_fp32(double offset + fp32
+// chunk-local prefix). The fp32 part is at most E + 6 + V additions deep, so
+// the relative error of a prefix of positive terms stays within a few ulps
+// however long the row is.
+//
+// Layout (both variants): a workgroup's chunk is W waves x 64 lanes x V
+// steps x E elements. Each wave owns a contiguous run of 64*V*E elements and
+// at step v its lanes read one lane-contiguous stretch of 64 16-byte
+// vectors, so every load and store instruction is fully coalesced.
 //
 // hw variant 0 (row-resident stream): one workgroup per row walks it chunk by
-//   chunk, carrying the double offset in registers. 1 read + 1 write.
+//   chunk, carrying the double offset. 1 read + 1 write.
 // hw variant 1 (split rows): rows are cut into chunks handled by separate
 //   workgroups. A first kernel writes each chunk's double total to the
-//   workspace; the second kernel adds the totals of the earlier chunks of its
-//   row and scans its own chunk. Reads the input twice (the second read
-//   mostly from the Infinity Cache), writes once; fills the GPU when there
-//   are few long rows (64 x 128256).
+//   workspace; the second adds the totals of the earlier chunks of its row and
+//   scans its own chunk. The input is read twice (the second read mostly from
+//   the Infinity Cache), written once; this fills the GPU when there are few
+//   long rows (64 x 128256).
 // Tile arguments: TILES_IN_BLOCK_M = W (waves per workgroup),
-//                 TILES_IN_BLOCK_N = V (16-byte vectors per thread per chunk).
+//                 TILES_IN_BLOCK_N = V (16-byte vectors per lane per chunk).
 #include "common.hpp"
 #include "registry.hpp"
 
@@ -28,28 +33,26 @@ namespace {
 
 constexpr int kMaxW = 16;
 
-// Loads thread `tid`'s V*E consecutive elements of chunk `c0` (blocked
-// layout), zero beyond n.
-template <typename T, int V, bool ALIGNED>
-__device__ __forceinline__ void load_run(const T* __restrict__ row, int64_t c0, int tid,
-                                         int64_t n, float (&x)[V * EPV<T>::value]) {
+// x[v][e] <- element (wbase + (v*64 + lane)*E + e) of `row`, zero past n.
+template <typename T, int V, bool ALIGNED, bool NT>
+__device__ __forceinline__ void load_striped(const T* __restrict__ row, int64_t wbase, int lane,
+                                             int64_t n, float (&x)[V][EPV<T>::value]) {
   constexpr int E = EPV<T>::value;
-  const int64_t base = c0 + static_cast<int64_t>(tid) * V * E;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
-    const int64_t off = base + v * E;
+    const int64_t off = wbase + static_cast<int64_t>(v * kWave + lane) * E;
     if constexpr (ALIGNED) {
-      if (off < n) {
-        const Vec<T> t = load_vec(row + off);
+      if (off < n) {  // n % E == 0: a vector is all in or all out
+        const Vec<T> t = NT ? load_vec_nt(row + off) : load_vec(row + off);
 #pragma unroll
-        for (int e = 0; e < E; ++e) x[v * E + e] = to_f32(t.v[e]);
+        for (int e = 0; e < E; ++e) x[v][e] = to_f32(t.v[e]);
       } else {
 #pragma unroll
-        for (int e = 0; e < E; ++e) x[v * E + e] = 0.f;
+        for (int e = 0; e < E; ++e) x[v][e] = 0.f;
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < E; ++e) x[v * E + e] = off + e < n ? to_f32(row[off + e]) : 0.f;
+      for (int e = 0; e < E; ++e) x[v][e] = off + e < n ? to_f32(row[off + e]) : 0.f;
     }
   }
 }
@@ -64,48 +67,60 @@ __device__ __forceinline__ float wave_incl_scan(float v, int lane) {
   return v;
 }
 
-// Scans the chunk held in x (in place, fp32 local inclusive prefixes), adds
-// the double `carry`, stores, and returns the chunk total in double (same on
-// every thread). Contains __syncthreads: every thread of the block calls it.
+// Turns x into wave-local inclusive prefixes (fp32) and returns the wave's
+// total (same on every lane).
+template <int V, int E>
+__device__ __forceinline__ float wave_scan_run(float (&x)[V][E], int lane) {
+  float run = 0.f;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+#pragma unroll
+    for (int e = 1; e < E; ++e) x[v][e] += x[v][e - 1];
+    const float t = x[v][E - 1];
+    const float incl = wave_incl_scan(t, lane);
+    const float base = run + (incl - t);
+#pragma unroll
+    for (int e = 0; e < E; ++e) x[v][e] += base;
+    run += __shfl(incl, kWave - 1, kWave);
+  }
+  return run;
+}
+
+// Scans the chunk held in x (striped), adds `carry`, stores, and returns the
+// chunk total in double (same on every thread). Contains __syncthreads:
+// every thread of the block calls it.
 template <typename T, int V, bool ALIGNED>
-__device__ __forceinline__ double scan_store_chunk(float (&x)[V * EPV<T>::value], T* __restrict__ orow,
+__device__ __forceinline__ double scan_store_chunk(float (&x)[V][EPV<T>::value], T* __restrict__ orow,
                                                    int64_t c0, int64_t n, double carry,
                                                    float* wave_tot) {
   constexpr int E = EPV<T>::value;
-  constexpr int R = V * E;
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid >> 6;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-#pragma unroll
-  for (int i = 1; i < R; ++i) x[i] += x[i - 1];
-  const float incl = wave_incl_scan(x[R - 1], lane);
-  const float excl_lane = incl - x[R - 1];
-  if (lane == kWave - 1) wave_tot[wave] = incl;
+  const float wt = wave_scan_run<V, E>(x, lane);
+  if (lane == 0) wave_tot[wave] = wt;
   __syncthreads();
-  float excl_wave = 0.f;
-  double total = 0.0;
+  double before = 0.0, total = 0.0;
   for (int w = 0; w < nw; ++w) {
-    const float t = wave_tot[w];
-    if (w < wave) excl_wave += t;
-    total += static_cast<double>(t);
+    const double t = static_cast<double>(wave_tot[w]);
+    if (w < wave) before += t;
+    total += t;
   }
   __syncthreads();  // wave_tot is rewritten by the next chunk
-  const float off_f = excl_wave + excl_lane;
-  const int64_t base = c0 + static_cast<int64_t>(tid) * R;
+  const double off = carry + before;
+  const int64_t wbase = c0 + static_cast<int64_t>(wave) * kWave * V * E;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
-    const int64_t off = base + v * E;
+    const int64_t o0 = wbase + static_cast<int64_t>(v * kWave + lane) * E;
     Vec<T> o;
 #pragma unroll
-    for (int e = 0; e < E; ++e)
-      o.v[e] = from_f32<T>(static_cast<float>(carry + static_cast<double>(x[v * E + e] + off_f)));
+    for (int e = 0; e < E; ++e) o.v[e] = from_f32<T>(static_cast<float>(off + static_cast<double>(x[v][e])));
     if constexpr (ALIGNED) {
-      if (off < n) store_vec(orow + off, o);
+      if (o0 < n) store_vec_nt(orow + o0, o);
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e)
-        if (off + e < n) orow[off + e] = o.v[e];
+        if (o0 + e < n) orow[o0 + e] = o.v[e];
     }
   }
   return total;
@@ -114,16 +129,18 @@ __device__ __forceinline__ double scan_store_chunk(float (&x)[V * EPV<T>::value]
 template <typename T, int V, bool ALIGNED>
 __global__ __launch_bounds__(1024) void scan_rows_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                          int64_t n) {
-  constexpr int R = V * EPV<T>::value;
+  constexpr int E = EPV<T>::value;
   __shared__ float wave_tot[kMaxW];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * n;
   T* yr = y + row * n;
-  const int64_t chunk = static_cast<int64_t>(blockDim.x) * R;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t per_wave = static_cast<int64_t>(kWave) * V * E;
+  const int64_t chunk = static_cast<int64_t>(blockDim.x >> 6) * per_wave;
   double carry = 0.0;
   for (int64_t c0 = 0; c0 < n; c0 += chunk) {
-    float v[R];
-    load_run<T, V, ALIGNED>(xr, c0, threadIdx.x, n, v);
+    float v[V][E];
+    load_striped<T, V, ALIGNED, true>(xr, c0 + (threadIdx.x >> 6) * per_wave, lane, n, v);
     carry += scan_store_chunk<T, V, ALIGNED>(v, yr, c0, n, carry, wave_tot);
   }
 }
@@ -132,18 +149,22 @@ template <typename T, int V, bool ALIGNED>
 __global__ __launch_bounds__(1024) void chunk_total_kernel(const T* __restrict__ x,
                                                            double* __restrict__ totals, int64_t n,
                                                            int nchunks) {
-  constexpr int R = V * EPV<T>::value;
+  constexpr int E = EPV<T>::value;
   __shared__ double wave_sum_lds[kMaxW];
   const int64_t row = blockIdx.y;
   const int c = blockIdx.x;
-  const int64_t chunk = static_cast<int64_t>(blockDim.x) * R;
-  float v[R];
-  load_run<T, V, ALIGNED>(x + row * n, c * chunk, threadIdx.x, n, v);
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int64_t per_wave = static_cast<int64_t>(kWave) * V * E;
+  const int64_t c0 = static_cast<int64_t>(c) * (blockDim.x >> 6) * per_wave;
+  float v[V][E];
+  // Regular (cached) loads: the scan pass re-reads this chunk right after.
+  load_striped<T, V, ALIGNED, false>(x + row * n, c0 + wave * per_wave, lane, n, v);
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < R; ++i) s += v[i];
-  double d = wave_sum(static_cast<double>(s));
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  for (int i = 0; i < V; ++i)
+#pragma unroll
+    for (int e = 0; e < E; ++e) s += v[i][e];
+  const double d = wave_sum(static_cast<double>(s));
   if (lane == 0) wave_sum_lds[wave] = d;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -157,14 +178,16 @@ template <typename T, int V, bool ALIGNED>
 __global__ __launch_bounds__(1024) void chunk_scan_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                           const double* __restrict__ totals,
                                                           int64_t n, int nchunks) {
-  constexpr int R = V * EPV<T>::value;
+  constexpr int E = EPV<T>::value;
   __shared__ float wave_tot[kMaxW];
   __shared__ double carry_lds;
   const int64_t row = blockIdx.y;
   const int c = blockIdx.x;
-  const int64_t chunk = static_cast<int64_t>(blockDim.x) * R;
-  float v[R];
-  load_run<T, V, ALIGNED>(x + row * n, c * chunk, threadIdx.x, n, v);
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int64_t per_wave = static_cast<int64_t>(kWave) * V * E;
+  const int64_t c0 = static_cast<int64_t>(c) * (blockDim.x >> 6) * per_wave;
+  float v[V][E];
+  load_striped<T, V, ALIGNED, true>(x + row * n, c0 + wave * per_wave, lane, n, v);
   if (threadIdx.x < kWave) {
     // Sum of the earlier chunk totals of this row, in double.
     double s = 0.0;
@@ -174,7 +197,7 @@ __global__ __launch_bounds__(1024) void chunk_scan_kernel(const T* __restrict__ 
   }
   __syncthreads();
   const double carry = carry_lds;
-  scan_store_chunk<T, V, ALIGNED>(v, y + row * n, c * chunk, n, carry, wave_tot);
+  scan_store_chunk<T, V, ALIGNED>(v, y + row * n, c0, n, carry, wave_tot);
 }
 
 // ---------------------------------------------------------------------------
@@ -243,12 +266,12 @@ void outputs_scan(const int64_t* dims, const int32_t* dtypes, OutDesc* out) {
   out[0] = {2, {dims[0], dims[1]}, dtypes[0]};
 }
 
-#define AXON_SCAN_PICK(KERNEL, T, A, V)      \
-  switch (V) {                               \
-    case 1: return KERNEL<T, 1, A>;          \
-    case 2: return KERNEL<T, 2, A>;          \
-    case 4: return KERNEL<T, 4, A>;          \
-    default: return KERNEL<T, 8, A>;         \
+#define AXON_SCAN_PICK(KERNEL, T, A, V) \
+  switch (V) {                          \
+    case 1: return KERNEL<T, 1, A>;     \
+    case 2: return KERNEL<T, 2, A>;     \
+    case 4: return KERNEL<T, 4, A>;     \
+    default: return KERNEL<T, 8, A>;    \
   }
 
 template <typename T, bool A>
@@ -274,7 +297,7 @@ int launch_scan_ta(const Call& c, const T* x, T* y, void* ws, hipStream_t st) {
   double* totals = static_cast<double*>(ws);
   const dim3 grid(nchunks, static_cast<unsigned>(m));
   hipLaunchKernelGGL((tot_fn<T, A>(V)), grid, block, 0, st, x, totals, n, nchunks);
-  int rc = launch_status("chunk_total_kernel");
+  const int rc = launch_status("chunk_total_kernel");
   if (rc != AXON_OK) return rc;
   hipLaunchKernelGGL((cscan_fn<T, A>(V)), grid, block, 0, st, x, y, totals, n, nchunks);
   return launch_status("chunk_scan_kernel");
@@ -297,8 +320,9 @@ int launch_scan(const Call& c, const void* const* in, void* const* out, void* ws
 
 const char* summary_scan(int variant) {
   return variant == 0
-             ? "row-resident stream: one workgroup per row, fp32 chunk scans (thread run, wave64 "
-               "shuffle scan, LDS wave totals) with a double carry; 1 read + 1 write"
+             ? "row-resident stream: one workgroup per row, striped coalesced chunks scanned in "
+               "fp32 (lane run, wave64 shuffle scan per step) with double wave/chunk offsets; "
+               "1 read + 1 write"
              : "split rows: chunk totals (double) to workspace, then each chunk adds its row's "
                "earlier totals and scans; fills the GPU for few long rows";
 }
