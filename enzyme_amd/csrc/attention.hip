@@ -10,22 +10,31 @@
 //
 // Schedule (hw variant 0): a workgroup of W waves owns 32*W query rows of one
 // (batch, head); each wave owns 32 of them and walks the key/value sequence
-// in blocks of BKV keys staged through double-buffered LDS (K as [key][d],
-// V transposed as [d][key]).
+// in blocks of BKV keys staged through double-buffered LDS.
 // Per block a wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (Q^T
 // held in registers for the whole walk), so each lane holds the scores of
 // ONE query (lane % 32) for 16 keys per 32-key tile: the row max and row
 // sum are in-lane reductions plus one exchange with lane ^ 32. The
-// probabilities P^T = exp2(S^T - m) are converted to bf16 in place and are
-// directly the B operand of O^T = V^T P^T; the MFMA's k index is mapped to
-// keys {0-3, 8-11 | 4-7, 12-15} (+16) to match the accumulator layout, and
-// V^T is read from LDS with the same key mapping. O^T keeps one query per
-// lane too, so the online-softmax rescale is a per-lane multiply.
-// Causal: key blocks past a wave's last query are skipped, only the diagonal
-// block is masked, and the heaviest query blocks are scheduled first.
+// probabilities P^T = exp2(S^T * scale*log2e - m) are converted to bf16 in
+// place and are directly the B operand of O^T = V^T P^T: the MFMA's k index
+// is mapped to keys {0-3, 8-11 | 4-7, 12-15} (+16) to match the accumulator
+// layout. V^T lives in LDS as [d][key] with bits 2 and 3 of the key index
+// swapped inside each 16-key group, so the 8 keys a lane needs for one MFMA
+// are one contiguous 16-byte read; it is written there as packed key pairs
+// (one 32-bit store per d, consecutive lanes on consecutive words, no bank
+// conflicts). K lives in LDS as [key][d] (16-byte stores and reads).
+// O^T keeps one query per lane too, so the online-softmax rescale is a
+// per-lane multiply; it is done only when some lane's running max grows by
+// more than 2^8 (a stale max leaves every probability <= 2^8, exact in the
+// fp32 sums and in bf16), which after the first block is almost never.
+// Causal: key blocks past a wave's last query are skipped, only blocks that
+// cross the diagonal (or the end of the sequence) are masked, and the
+// heaviest query blocks are scheduled first; the heads are dealt to the 8
+// XCDs so each XCD's L2 serves the K/V of h/8 heads only.
 // Tile arguments: TILES_IN_BLOCK_M = W (waves, 32 queries each),
 //                 TILES_IN_BLOCK_N = BKV / 32; K and P are pinned to 1.
 #include <atomic>
+#include <type_traits>
 
 #include "common.hpp"
 #include "registry.hpp"
@@ -38,8 +47,10 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int D = 128;
-constexpr int KP = D + 8;  // Ks row pitch (elements)
+constexpr int KP = D + 8;  // Ks row pitch (elements): 16-byte reads of 8 rows hit 32 banks
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleSlack = 8.f;  // log2 of the largest un-rescaled probability
+constexpr int kXcds = 8;
 
 struct AttnArgs {
   const bf16* q;   // [BH][s][D]
@@ -49,17 +60,34 @@ struct AttnArgs {
   int s;
   int bh;
   int qblocks;
+  int xcd_heads;     // heads per XCD when the XCD mapping applies, else 0
   float scale_log2;  // softmax scale * log2(e)
 };
+
+// Position of key k (0..15 inside its 16-key group) in a V^T row: bits 2 and
+// 3 swapped, so keys {0-3, 8-11} and {4-7, 12-15} are contiguous.
+__device__ __forceinline__ int vt_pos(int k) {
+  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+__device__ __forceinline__ uint32_t pack2(bf16 lo, bf16 hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+}
 
 template <int W, int TN, bool CAUSAL, bool KT>
 __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
   constexpr int BQ = 32 * W;
   constexpr int BKV = 32 * TN;
-  constexpr int VP = BKV + 8;         // Vt row pitch (elements)
+  constexpr int VP = BKV + 8;  // Vt row pitch (elements)
   constexpr int NT = W * 64;
-  constexpr int KR = BKV / (4 * W);   // keys (or d rows) per thread per block load
-  static_assert(KR >= 1 && KR <= 8, "tile shape");
+  // K staging (row layout): BKV*D/8 16-byte vectors.
+  constexpr int KITEMS = KT ? (D / 2) * (BKV / 8) : BKV * D / 8;
+  constexpr int KI = (KITEMS + NT - 1) / NT;
+  // V staging: (BKV/2 key pairs) x (D/8 chunks), two 16-byte loads each.
+  constexpr int VITEMS = (BKV / 2) * (D / 8);
+  constexpr int VI = (VITEMS + NT - 1) / NT;
+  constexpr int KL = KT ? 2 : 1;  // 16-byte loads per K item
 
   extern __shared__ __align__(16) unsigned char smem[];
   bf16* Ks = reinterpret_cast<bf16*>(smem);  // [2][BKV][KP]
@@ -70,10 +98,20 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
   const int wave = tid >> 6;
   const int h = lane >> 5;  // half of the wave
 
-  // Heaviest (latest) query blocks first under causal masking.
-  const int qb = CAUSAL ? (a.qblocks - 1 - static_cast<int>(blockIdx.x) % a.qblocks)
-                        : static_cast<int>(blockIdx.x) % a.qblocks;
-  const int bh = static_cast<int>(blockIdx.x) / a.qblocks;
+  // Block -> (head, query block): heaviest (latest) query blocks first under
+  // causal masking; with the XCD mapping, block b runs on XCD b % 8 and that
+  // XCD only ever sees heads x, x+8, x+16, ...
+  int rank, bh;
+  const int bid = static_cast<int>(blockIdx.x);
+  if (a.xcd_heads > 0) {
+    const int x = bid % kXcds, j = bid / kXcds;
+    rank = j / a.xcd_heads;
+    bh = x + kXcds * (j % a.xcd_heads);
+  } else {
+    rank = bid % a.qblocks;
+    bh = bid / a.qblocks;
+  }
+  const int qb = CAUSAL ? a.qblocks - 1 - rank : rank;
   const int64_t base = static_cast<int64_t>(bh) * a.s * D;
   const bf16* Q = a.q + base;
   const bf16* K = a.k + base;
@@ -96,62 +134,74 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
       for (int i = 0; i < 8; ++i) qf[st][i] = static_cast<bf16>(0.f);
   }
 
-  // Global -> register staging of one K/V block.
-  Vec<bf16> kreg[KR], vreg[KR];
-  // K (row layout [key][d]): vector v = tid + i*NT -> key v/16, d chunk v%16.
-  // K^T layout [d][key]: thread -> d rows (tid % (D/KR))*KR.., keys chunk
-  //   (tid / (D/KR))*8 .. +8 -- transposed into Ks on store.
-  // V: thread -> keys (tid / 16)*KR .. +KR, d chunk (tid % 16)*8.
+  // Global -> register staging of one K/V block (zeros past the sequence).
+  Vec<bf16> kreg[KI][KL], vreg[VI][2];
+  auto zero_vec = [](Vec<bf16>& r) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.v[e] = static_cast<bf16>(0.f);
+  };
   auto load_block = [&](int kv0) {
 #pragma unroll
-    for (int i = 0; i < KR; ++i) {
+    for (int i = 0; i < KI; ++i) {
+      const int item = tid + i * NT;
+      if (KITEMS % NT != 0 && item >= KITEMS) continue;
       if constexpr (!KT) {
-        const int v = tid + i * NT;
-        const int key = kv0 + (v >> 4), dc = (v & 15) * 8;
-        if (key < a.s) kreg[i] = load_vec(K + static_cast<int64_t>(key) * D + dc);
-        else for (int e = 0; e < 8; ++e) kreg[i].v[e] = static_cast<bf16>(0.f);
+        // item -> key item/16, d chunk (item%16)*8
+        const int key = kv0 + (item >> 4), dc = (item & 15) * 8;
+        if (key < a.s) kreg[i][0] = load_vec(K + static_cast<int64_t>(key) * D + dc);
+        else zero_vec(kreg[i][0]);
       } else {
-        const int dr = (tid % (D / KR)) * KR + i;
-        const int key = kv0 + (tid / (D / KR)) * 8;
-        if (key + 7 < a.s) {
-          kreg[i] = load_vec(K + static_cast<int64_t>(dr) * a.s + key);
-        } else {
-          for (int e = 0; e < 8; ++e)
-            kreg[i].v[e] = key + e < a.s ? K[static_cast<int64_t>(dr) * a.s + key + e] : static_cast<bf16>(0.f);
+        // item -> d pair dp = item % 64, key chunk kc = item / 64 (s % 8 == 0)
+        const int dp = item % (D / 2), key = kv0 + (item / (D / 2)) * 8;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          if (key < a.s) kreg[i][r] = load_vec(K + static_cast<int64_t>(2 * dp + r) * a.s + key);
+          else zero_vec(kreg[i][r]);
         }
       }
-      const int key = kv0 + (tid >> 4) * KR + i;
-      const int dc = (tid & 15) * 8;
-      if (key < a.s) vreg[i] = load_vec(V + static_cast<int64_t>(key) * D + dc);
-      else for (int e = 0; e < 8; ++e) vreg[i].v[e] = static_cast<bf16>(0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      const int item = tid + i * NT;
+      if (VITEMS % NT != 0 && item >= VITEMS) continue;
+      // item -> key pair p = item % (BKV/2), d chunk c = item / (BKV/2)
+      const int p = item % (BKV / 2), c = item / (BKV / 2);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int key = kv0 + 2 * p + r;
+        if (key < a.s) vreg[i][r] = load_vec(V + static_cast<int64_t>(key) * D + c * 8);
+        else zero_vec(vreg[i][r]);
+      }
     }
   };
 
   auto store_block = [&](int buf) {
     bf16* ks = Ks + buf * BKV * KP;
     bf16* vt = Vt + buf * D * VP;
-    if constexpr (!KT) {
 #pragma unroll
-      for (int i = 0; i < KR; ++i) {
-        const int v = tid + i * NT;
-        store_vec(ks + (v >> 4) * KP + (v & 15) * 8, kreg[i]);
+    for (int i = 0; i < KI; ++i) {
+      const int item = tid + i * NT;
+      if (KITEMS % NT != 0 && item >= KITEMS) continue;
+      if constexpr (!KT) {
+        store_vec(ks + (item >> 4) * KP + (item & 15) * 8, kreg[i][0]);
+      } else {
+        const int dp = item % (D / 2), kc = (item / (D / 2)) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          *reinterpret_cast<uint32_t*>(ks + (kc + e) * KP + 2 * dp) = pack2(kreg[i][0].v[e], kreg[i][1].v[e]);
       }
-    } else {
-      // kreg[i] holds d row dr0+i for keys kc..kc+7: write each key's KR d-values.
-      const int dr0 = (tid % (D / KR)) * KR;
-      const int kc = (tid / (D / KR)) * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      const int item = tid + i * NT;
+      if (VITEMS % NT != 0 && item >= VITEMS) continue;
+      const int p = item % (BKV / 2), c = item / (BKV / 2);
+      const int k0 = 2 * p;
+      const int pos = (k0 & ~15) | vt_pos(k0 & 15);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-#pragma unroll
-        for (int i = 0; i < KR; ++i) ks[(kc + e) * KP + dr0 + i] = kreg[i].v[e];
+        *reinterpret_cast<uint32_t*>(vt + (c * 8 + e) * VP + pos) = pack2(vreg[i][0].v[e], vreg[i][1].v[e]);
     }
-    // V transposed: d row dc+e gets keys kb..kb+KR-1.
-    const int kb = (tid >> 4) * KR;
-    const int dc = (tid & 15) * 8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int i = 0; i < KR; ++i) vt[(dc + e) * VP + kb + i] = vreg[i].v[e];
   };
 
   floatx16 acc_o[D / 32];
@@ -160,6 +210,70 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc_o[t][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
+
+  // One key block for this wave; MASK applies the causal / sequence-end mask.
+  auto process = [&](auto mask_tag, const bf16* ks, const bf16* vt, int kv0) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    // S^T = K Q^T: acc_s[t] rows = keys t*32.., columns = this wave's queries.
+    floatx16 acc_s[TN];
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc_s[t][e] = 0.f;
+#pragma unroll
+      for (int st = 0; st < D / 16; ++st) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + (t * 32 + (lane & 31)) * KP + st * 16 + h * 8);
+        acc_s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], acc_s[t], 0, 0, 0);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        if constexpr (MASK) {
+          const int key = kv0 + t * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+          if ((CAUSAL && key > my_q) || key >= a.s) acc_s[t][e] = -INFINITY;
+        }
+        mx = fmaxf(mx, acc_s[t][e]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mxs = mx * a.scale_log2;
+    if (__any(mxs > m_run + kRescaleSlack)) {
+      const float m_new = fmaxf(m_run, mxs);
+      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_o[dt][e] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    // P^T in bf16, grouped by MFMA k-step: pf[t][ks] holds keys
+    // t*32 + ks*16 + {0-3, 8-11} (h = 0) or {4-7, 12-15} (h = 1).
+    float lblk = 0.f;
+    bf16x8 pf[TN][2];
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[t][e], a.scale_log2, -m_use));
+        lblk += p;
+        pf[t][e >> 3][e & 7] = static_cast<bf16>(p);
+      }
+    l_run += lblk + __shfl_xor(lblk, 32, 64);
+    // O^T += V^T P^T; the V^T fragment is one 16-byte read (permuted keys).
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vt + (dt * 32 + (lane & 31)) * VP + t * 32 + ks2 * 16 + 8 * h);
+          acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][ks2], acc_o[dt], 0, 0, 0);
+        }
+  };
 
   if (nblocks > 0) {
     load_block(0);
@@ -172,78 +286,12 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
     const int kv0 = blk * BKV;
     if (blk + 1 < nblocks) load_block(kv0 + BKV);
 
-    const bool active = !CAUSAL || kv0 <= qw + 31;
-    if (active && qw < a.s) {
+    if ((!CAUSAL || kv0 <= qw + 31) && qw < a.s) {
       const bf16* ks = Ks + buf * BKV * KP;
       const bf16* vt = Vt + buf * D * VP;
-      // S^T = K Q^T: acc_s[t] rows = keys t*32.., columns = this wave's queries.
-      floatx16 acc_s[TN];
-#pragma unroll
-      for (int t = 0; t < TN; ++t) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc_s[t][e] = 0.f;
-#pragma unroll
-        for (int st = 0; st < D / 16; ++st) {
-          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + (t * 32 + (lane & 31)) * KP + st * 16 + h * 8);
-          acc_s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], acc_s[t], 0, 0, 0);
-        }
-      }
-      // Scale, mask, block max for this lane's query.
-      const bool diag = CAUSAL && kv0 + BKV - 1 > qw;
-      float mblk = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < TN; ++t)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = kv0 + t * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-          float x = acc_s[t][e] * a.scale_log2;
-          if ((diag && key > my_q) || key >= a.s) x = -INFINITY;
-          acc_s[t][e] = x;
-          mblk = fmaxf(mblk, x);
-        }
-      mblk = fmaxf(mblk, __shfl_xor(mblk, 32, 64));
-      const float m_new = fmaxf(m_run, mblk);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
-      float lblk = 0.f;
-      // P^T in bf16, grouped by MFMA k-step: pf[t][ks] holds keys
-      // t*32 + ks*16 + {0-3, 8-11} (h = 0) or {4-7, 12-15} (h = 1).
-      bf16x8 pf[TN][2];
-#pragma unroll
-      for (int t = 0; t < TN; ++t)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float p = exp2f(acc_s[t][e] - m_use);
-          lblk += p;
-          pf[t][e >> 3][e & 7] = static_cast<bf16>(p);
-        }
-      lblk += __shfl_xor(lblk, 32, 64);
-      l_run = l_run * alpha + lblk;
-      m_run = m_new;
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc_o[dt][e] *= alpha;
-      // O^T += V^T P^T.
-#pragma unroll
-      for (int t = 0; t < TN; ++t)
-#pragma unroll
-        for (int ks2 = 0; ks2 < 2; ++ks2) {
-          const int kb = t * 32 + ks2 * 16 + 4 * h;
-#pragma unroll
-          for (int dt = 0; dt < D / 32; ++dt) {
-            const bf16* row = vt + (dt * 32 + (lane & 31)) * VP + kb;
-            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row);
-            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 8);
-            bf16x8 vf;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              vf[i] = lo[i];
-              vf[4 + i] = hi[i];
-            }
-            acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][ks2], acc_o[dt], 0, 0, 0);
-          }
-        }
+      const bool mask = (CAUSAL && kv0 + BKV - 1 > qw) || kv0 + BKV > a.s;
+      if (mask) process(std::true_type{}, ks, vt, kv0);
+      else process(std::false_type{}, ks, vt, kv0);
     }
     // The other buffer was last read before the previous barrier.
     if (blk + 1 < nblocks) store_block(buf ^ 1);
@@ -286,9 +334,11 @@ int check_tiles(const Call& c, std::string* why) {
     *why = "TILES_IN_BLOCK_N (key block / 32) must be 1, 2 or 4";
     return AXON_EINVAL;
   }
-  // Each thread stages KR = BKV / (4 W) keys (or k_t rows) per block.
-  if (32 * TN % (4 * W) != 0 || 32 * TN / (4 * W) > 8) {
-    *why = "the key block must satisfy 4 x waves <= BKV <= 32 x waves";
+  // Per block each thread stages ceil(8*TN/W) K vectors and 2*ceil(4*TN/W)
+  // V vectors in registers; more than 8 would crowd out the accumulators.
+  const int ki = (8 * TN + W - 1) / W, vi = (4 * TN + W - 1) / W;
+  if (ki + 2 * vi > 8) {
+    *why = "the key block stages more than 8 vectors per thread: need 32*waves >= 8*BKV/8";
     return AXON_EINVAL;
   }
   if (c.tile(2) != 1 || c.tile(3) != 1) {
@@ -384,7 +434,7 @@ int launch_t(const AttnArgs& a, hipStream_t st) {
   auto fn = attn_kernel<W, TN, CAUSAL, KT>;
   static std::atomic<bool> configured{false};
   if (!configured.load(std::memory_order_acquire)) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                         static_cast<int>(lds));
     configured.store(true, std::memory_order_release);
   }
@@ -431,6 +481,8 @@ int launch_common(const Call& c, const void* const* in, void* const* out, hipStr
     set_error("grid too large");
     return AXON_EINVAL;
   }
+  // Deal heads to XCDs (workgroup b runs on XCD b % 8) when they split evenly.
+  a.xcd_heads = a.bh % kXcds == 0 ? a.bh / kXcds : 0;
   if (causal) {
     a.scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
     return dispatch<true, false>(W, TN, a, st);

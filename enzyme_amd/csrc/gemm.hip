@@ -494,7 +494,7 @@ void launch_tile(const GemmArgs& g, hipStream_t st) {
   // doing it for the first time is harmless.
   static std::atomic<bool> configured{false};
   if (!configured.load(std::memory_order_acquire)) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                         static_cast<int>(lds));
     configured.store(true, std::memory_order_release);
   }
