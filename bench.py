@@ -49,7 +49,7 @@ METRIC = "achieved HBM GB/s (% peak) per norm/rope/scan; MFMA TFLOP/s for matmul
 # algorithmic work per launch (bytes for "hbm", FLOPs for "mfma"), label.
 CONFIGS = [
     dict(
-        spec="rope_llama3", sizes=(1, 4096, 32, 8, 128), variant=0, tiles=(2, 1), bound="hbm",
+        spec="rope_llama3", sizes=(1, 4096, 32, 8, 128), variant=0, tiles=(4, 1), bound="hbm",
         work=88_080_384,
         label="RoPE Llama-3-8B: q[1,4096,32,128] k[1,4096,8,128] bf16, cos/sin[4096,128] fp32, theta 500000",
     ),
@@ -59,17 +59,17 @@ CONFIGS = [
         label="RMSNorm x[2048,4096] bf16, weight[4096] bf16, eps 1e-6",
     ),
     dict(
-        spec="cumsum_probs", sizes=(64, 128256), variant=1, tiles=(8, 1), bound="hbm",
+        spec="cumsum_probs", sizes=(64, 128256), variant=2, tiles=(8, 4), bound="hbm",
         work=65_667_072,
         label="cumsum over vocab: probs[64,128256] fp32 (sorted softmax of N(0,3) logits)",
     ),
     dict(
-        spec="matmul_std002", sizes=(1024, 512, 16384), variant=0, tiles=(2, 2, 32), bound="mfma",
+        spec="matmul_std002", sizes=(1024, 512, 16384), variant=0, tiles=(4, 4, 4), bound="mfma",
         work=2 * 1024 * 512 * 16384,
         label="matmul m,n,k = 1024,512,16384 bf16 N(0,0.02), fp32 accumulate",
     ),
     dict(
-        spec="rmsnorm_matmul_eps", sizes=(1024, 512, 16384), variant=0, tiles=(2, 2, 32), bound="mfma",
+        spec="rmsnorm_matmul_eps", sizes=(1024, 512, 16384), variant=0, tiles=(4, 4, 4), bound="mfma",
         work=2 * 1024 * 512 * 16384,
         label="rmsnorm_matmul m,n,k = 1024,512,16384 bf16, eps 1e-6",
     ),

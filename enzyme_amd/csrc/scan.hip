@@ -23,8 +23,20 @@
 //   scans its own chunk. The input is read twice (the second read mostly from
 //   the Infinity Cache), written once; this fills the GPU when there are few
 //   long rows (64 x 128256).
+// hw variant 2 (single pass, published chunk totals): one launch, 1 read +
+//   1 write. Workgroup b owns chunk b (row-major), loads it, publishes its
+//   chunk total as one 64-bit word {launch tag, fp32 total} and sums the
+//   totals of the earlier chunks of its row as they appear (one poll round
+//   per lane in the common case). The tag is unique per launch (a counter in
+//   the library), so words left by earlier launches never match and the
+//   workspace needs no reset. Workgroups are dispatched in index order on
+//   each XCD, so a workgroup only waits for workgroups that are running or
+//   done; the polls are bounded anyway (an exhausted bound sets the error
+//   word in the workspace header and the kernel still finishes).
 // Tile arguments: TILES_IN_BLOCK_M = W (waves per workgroup),
 //                 TILES_IN_BLOCK_N = V (16-byte vectors per lane per chunk).
+#include <atomic>
+
 #include "common.hpp"
 #include "registry.hpp"
 
@@ -200,6 +212,81 @@ __global__ __launch_bounds__(1024) void chunk_scan_kernel(const T* __restrict__ 
   scan_store_chunk<T, V, ALIGNED>(v, y + row * n, c0, n, carry, wave_tot);
 }
 
+// Single-pass workspace: a header (word 0: poll-bound error flag) padded to
+// 256 bytes, then one 64-bit slot per chunk (row-major).
+constexpr size_t kOnepassHeader = 256;
+constexpr unsigned kMaxPolls = 1u << 16;
+
+template <typename T, int V, bool ALIGNED>
+__global__ __launch_bounds__(1024) void scan_onepass_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                            unsigned* hdr, unsigned long long* slots,
+                                                            int64_t n, int nchunks, unsigned tag) {
+  constexpr int E = EPV<T>::value;
+  __shared__ float wave_tot[kMaxW];
+  __shared__ double part[kMaxW];
+  __shared__ double s_carry;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  const unsigned b = blockIdx.x;
+  const int64_t row = b / static_cast<unsigned>(nchunks);
+  const int c = static_cast<int>(b - row * nchunks);
+  const int64_t per_wave = static_cast<int64_t>(kWave) * V * E;
+  const int64_t c0 = static_cast<int64_t>(c) * nw * per_wave;
+  float v[V][E];
+  load_striped<T, V, ALIGNED, true>(x + row * n, c0 + wave * per_wave, lane, n, v);
+
+  // Publish this chunk's total (not needed by the last chunk of a row).
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+#pragma unroll
+    for (int e = 0; e < E; ++e) s += v[i][e];
+  const double d = wave_sum(static_cast<double>(s));
+  if (lane == 0) part[wave] = d;
+  __syncthreads();
+  if (threadIdx.x == 0 && c + 1 < nchunks) {
+    double t = 0.0;
+    for (int w = 0; w < nw; ++w) t += part[w];
+    const unsigned long long word =
+        (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(static_cast<float>(t));
+    __hip_atomic_store(&slots[b], word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // Carry: the totals of chunks 0..c-1 of this row (wave 0, one chunk per lane).
+  if (wave == 0) {
+    double acc = 0.0;
+    const int64_t rowbase = row * nchunks;
+    for (int i = lane; i < c; i += kWave) {
+      unsigned long long w = 0;
+      for (unsigned polls = 0;; ++polls) {
+        w = __hip_atomic_load(&slots[rowbase + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (static_cast<unsigned>(w >> 32) == tag) break;
+        if (polls == kMaxPolls) {
+          __hip_atomic_store(&hdr[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          w = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      acc += static_cast<double>(__uint_as_float(static_cast<unsigned>(w)));
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) s_carry = acc;
+  }
+  __syncthreads();
+  scan_store_chunk<T, V, ALIGNED>(v, y + row * n, c0, n, s_carry, wave_tot);
+}
+
+// Launch tags of the single-pass variant: unique per launch in this process
+// (0 is never used, so a zero-filled workspace matches nothing).
+std::atomic<unsigned> g_scan_tag{0};
+
+unsigned next_scan_tag() {
+  unsigned t = g_scan_tag.fetch_add(1, std::memory_order_relaxed) + 1;
+  if (t == 0) t = g_scan_tag.fetch_add(1, std::memory_order_relaxed) + 1;
+  return t;
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -238,6 +325,13 @@ int check_scan(const Call& c, std::string* why) {
       return AXON_EINVAL;
     }
   }
+  if (c.variant == 2) {
+    const int64_t nchunks = (c.dim(1) + chunk_elems(c) - 1) / chunk_elems(c);
+    if (c.dim(0) * nchunks > (1LL << 31) - 1) {
+      *why = "single-pass scan needs fewer than 2^31 chunks in total";
+      return AXON_EINVAL;
+    }
+  }
   return AXON_OK;
 }
 
@@ -249,7 +343,7 @@ int manifest_scan(int variant, const int64_t* dims, int dtype, Constraint* out, 
   // vectors (variant 0), or more than a quarter of them (variant 1, so each
   // row splits into at least a few chunks).
   int64_t lanes = (n + E - 1) / E;
-  if (variant == 1) lanes = lanes / 4 > 0 ? lanes / 4 : 1;
+  if (variant >= 1) lanes = lanes / 4 > 0 ? lanes / 4 : 1;
   const int64_t w = (lanes + kWave - 1) / kWave;
   out[0] = {"TILES_IN_BLOCK_M", w < kMaxW ? w : kMaxW, 1, false};
   out[1] = {"TILES_IN_BLOCK_N", 8, 1, false};
@@ -257,9 +351,10 @@ int manifest_scan(int variant, const int64_t* dims, int dtype, Constraint* out, 
 }
 
 size_t workspace_scan(const Call& c) {
-  if (c.variant != 1) return 0;
+  if (c.variant == 0) return 0;
   const int64_t nchunks = (c.dim(1) + chunk_elems(c) - 1) / chunk_elems(c);
-  return static_cast<size_t>(c.dim(0) * nchunks) * sizeof(double);
+  const size_t slots = static_cast<size_t>(c.dim(0) * nchunks) * 8;  // double / 64-bit word
+  return c.variant == 1 ? slots : kOnepassHeader + slots;
 }
 
 void outputs_scan(const int64_t* dims, const int32_t* dtypes, OutDesc* out) {
@@ -282,6 +377,10 @@ template <typename T, bool A>
 void (*cscan_fn(int V))(const T*, T*, const double*, int64_t, int) {
   AXON_SCAN_PICK(chunk_scan_kernel, T, A, V)
 }
+template <typename T, bool A>
+void (*onepass_fn(int V))(const T*, T*, unsigned*, unsigned long long*, int64_t, int, unsigned) {
+  AXON_SCAN_PICK(scan_onepass_kernel, T, A, V)
+}
 
 template <typename T, bool A>
 int launch_scan_ta(const Call& c, const T* x, T* y, void* ws, hipStream_t st) {
@@ -294,6 +393,14 @@ int launch_scan_ta(const Call& c, const T* x, T* y, void* ws, hipStream_t st) {
   }
   const int64_t ce = chunk_elems(c);
   const int nchunks = static_cast<int>((n + ce - 1) / ce);
+  if (c.variant == 2) {
+    const unsigned nblocks = static_cast<unsigned>(m * nchunks);
+    unsigned* hdr = static_cast<unsigned*>(ws);
+    auto* slots = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + kOnepassHeader);
+    hipLaunchKernelGGL((onepass_fn<T, A>(V)), dim3(nblocks), block, 0, st, x, y, hdr, slots, n,
+                       nchunks, next_scan_tag());
+    return launch_status("scan_onepass_kernel");
+  }
   double* totals = static_cast<double*>(ws);
   const dim3 grid(nchunks, static_cast<unsigned>(m));
   hipLaunchKernelGGL((tot_fn<T, A>(V)), grid, block, 0, st, x, totals, n, nchunks);
@@ -319,6 +426,10 @@ int launch_scan(const Call& c, const void* const* in, void* const* out, void* ws
 }
 
 const char* summary_scan(int variant) {
+  if (variant == 2)
+    return "single pass: each chunk publishes a {launch tag, fp32 total} word and adds the "
+           "published totals of its row's earlier chunks (double carry); 1 read + 1 write, one "
+           "launch";
   return variant == 0
              ? "row-resident stream: one workgroup per row, striped coalesced chunks scanned in "
                "fp32 (lane run, wave64 shuffle scan per step) with double wave/chunk offsets; "
@@ -330,13 +441,13 @@ const char* summary_scan(int variant) {
 }  // namespace
 
 const Family* family_cumsum() {
-  static const Family f = {"cumsum", 2, 1, 1, 2, kTileArgs, 2, summary_scan, manifest_scan,
+  static const Family f = {"cumsum", 3, 1, 1, 2, kTileArgs, 2, summary_scan, manifest_scan,
                            check_scan, workspace_scan, outputs_scan, launch_scan};
   return &f;
 }
 
 const Family* family_cumsum_probs() {
-  static const Family f = {"cumsum_probs", 2, 1, 1, 2, kTileArgs, 2, summary_scan, manifest_scan,
+  static const Family f = {"cumsum_probs", 3, 1, 1, 2, kTileArgs, 2, summary_scan, manifest_scan,
                            check_scan, workspace_scan, outputs_scan, launch_scan};
   return &f;
 }

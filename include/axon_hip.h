@@ -106,7 +106,11 @@ int axon_variant_check(const char* kernel, int hw_variant,
                        const int64_t* dims, int n_dims,
                        const int32_t* dtypes, int n_dtypes);
 
-/* Bytes of device workspace one launch needs (0 for most variants). */
+/* Bytes of device workspace one launch needs (0 for most variants). A
+ * workspace must be zero-filled before its first launch; every launch leaves
+ * it ready for the next one (the single-pass cumsum variant keeps an error
+ * word there, set only if a poll bound ran out). Launches that overlap on one
+ * workspace race. */
 size_t axon_variant_workspace(const char* kernel, int hw_variant,
                               const int32_t* tiles, int n_tiles,
                               const int64_t* dims, int n_dims,

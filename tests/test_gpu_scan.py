@@ -45,3 +45,26 @@ def test_sequential_fp32_drift_exceeds_bound():
     p = torch.as_tensor(probs)
     rel = ((oracle.cumsum_seq_f32(p) - oracle.cumsum(p)).abs() / oracle.cumsum(p)).max()
     assert rel > 1e-5
+
+
+@pytest.mark.parametrize("tiles", [(2, 4), (4, 8), (1, 1)])
+def test_single_pass_reuses_workspace(tiles):
+    """hw variant 2 publishes chunk totals tagged with a per-launch tag in its
+    workspace: back-to-back launches on one workspace, with the input
+    changed in between, must each be right (a stale total from the previous
+    launch would be off), and the poll-bound error word stays clear."""
+    from enzyme_amd import hip
+    from tests._specs import spec_inputs, to_device
+
+    spec, dims, host = spec_inputs("cumsum_probs", (7, 20000))
+    dev = to_device(host)
+    ln = hip.Launcher("cumsum_probs", 2, tiles, [dims[d] for d in spec.dim_vars], dev)
+    for i in range(4):
+        if i:
+            dev[0].mul_(0.5 if i % 2 else 3.0)
+        want = oracle.cumsum(dev[0].cpu())
+        ln.outputs[0].fill_(float("nan"))
+        ln.launch()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(ln.outputs[0].cpu(), want, rtol=1e-5, atol=0.0)
+        assert int(ln.workspace[:4].view(torch.int32).item()) == 0, f"launch {i}: poll bound hit"
