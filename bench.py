@@ -125,6 +125,32 @@ def measure(cfg: dict, steps: int, warmup: int):
     return avg_us, outs, host, spec
 
 
+def measure_copy(nbytes: int, steps: int, warmup: int) -> float:
+    """Average duration (us) of a plain 16-byte-vector device copy that reads
+    and writes `nbytes` each, rotating over >= 1 GiB of buffer pairs: the
+    practical HBM ceiling for a kernel moving 2 * nbytes."""
+    import torch
+
+    from enzyme_amd import hip
+
+    nbytes = max(16, nbytes // 16 * 16)
+    n_sets = max(2, min(64, math.ceil(ROTATE_BYTES / (2 * nbytes))))
+    sets = [(torch.empty(nbytes, dtype=torch.uint8, device="cuda"),
+             torch.empty(nbytes, dtype=torch.uint8, device="cuda")) for _ in range(n_sets)]
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        hip.copy(*sets[i % n_sets])
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        hip.copy(*sets[i % n_sets])
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / steps
+
+
 def cpu_baseline(cfg: dict, host, gpu_outs, runs: int = 10):
     """The oracle on the host cores: (median seconds, threads, max error of
     the GPU output against it)."""
@@ -222,6 +248,15 @@ def main(argv=None) -> int:
     rf["traffic"] = traffic_for(head["spec"])
     line["value"] = rf["achieved"]
     line["roofline"] = rf
+    copy_us = measure_copy(head["work"] // 2, args.steps, args.warmup)
+    line["copy_ceiling"] = {
+        "us": round(copy_us, 3),
+        "achieved": round(head["work"] / (copy_us * 1e-6) / 1e9, 2),
+        "unit": "GB/s",
+        "what": "plain 16-byte-vector copy reading and writing half the headline's algorithmic "
+                "bytes each, same buffer rotation: the HBM rate a streaming kernel of this size "
+                "reaches here",
+    }
     if not args.no_cpu:
         sec, threads, err, ok = cpu_baseline(head, host, outs)
         line["cpu_baseline"] = {
@@ -240,7 +275,12 @@ def main(argv=None) -> int:
             steps = max(20, args.steps // (4 if cfg["bound"] == "mfma" else 1))
             us, o, h, _ = measure(cfg, steps, args.warmup)
             row = {"spec": cfg["spec"], "label": cfg["label"], "tiles": list(cfg["tiles"]),
-                   "hw_variant": cfg["variant"], "us_per_launch": round(us, 3), **roofline(cfg, us)}
+                   "hw_variant": cfg["variant"], "us_per_launch": round(us, 3), **roofline(cfg, us),
+                   "traffic": traffic_for(cfg["spec"])}
+            if cfg["bound"] == "hbm":
+                cu = measure_copy(cfg["work"] // 2, steps, args.warmup)
+                row["copy_us"] = round(cu, 3)
+                row["vs_copy"] = round(cu / us, 4)
             if not args.no_cpu:
                 runs = 3 if cfg["spec"] == "attention_causal" else 10
                 sec, threads, err, ok = cpu_baseline(cfg, h, o, runs=runs)
