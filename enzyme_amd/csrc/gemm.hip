@@ -26,6 +26,14 @@
 // XCD (blocks are dealt round-robin over the 8 XCDs), keeping that range of A
 // and B in one L2.
 //
+// hw variant 1 keeps PD register sets of global loads in flight (PD = 3 for
+// tiles up to 128 x 128, 2 above) and stages B as loaded, [k][n], so every
+// B load instruction reads whole 128-byte lines (variant 0's transposing
+// register staging reads half lines, and a CU's vector L1 delivers about
+// half the useful bytes per cycle on half lines). The MFMA B fragments then
+// come from gfx950's transposing LDS read (ds_read_b64_tr_b16): two reads
+// give a lane the 8 consecutive k values of its column.
+//
 // Tile arguments: TILES_IN_BLOCK_M = BM/32, TILES_IN_BLOCK_N = BN/32,
 //                 TILES_IN_BLOCK_K = K range per workgroup / 256
 //                 (silu_mlp: TILES_IN_BLOCK_P = BN/32 of its second GEMM).
@@ -40,10 +48,17 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int BK = 64;
 constexpr int kKUnit = 256;  // TILES_IN_BLOCK_K counts K in units of 256
 constexpr int LDK = BK + 8;  // LDS row pitch in elements (144 B; keeps 16 B alignment)
+
+// Row pitch (elements) of the [k][n] B tile of hw variant 1: BN + 16 puts the
+// four k rows one transposing read touches 8 banks apart.
+constexpr int bpitch(int BN) { return BN + 16; }
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
 
@@ -64,7 +79,10 @@ struct GemmArgs {
 
 __device__ __forceinline__ float silu(float a) { return a / (1.f + __expf(-a)); }
 
-template <int BM, int BN, int EPI, bool A_F32>
+template <int N>
+using ic = std::integral_constant<int, N>;
+
+template <int BM, int BN, int EPI, bool A_F32, int PD>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   constexpr bool DUAL = EPI == kSiluMul;
   constexpr int WM = BM / 2, WN = BN / 2;  // per-wave tile
@@ -76,8 +94,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   static_assert(AV >= 1 && KR >= 2 && KR <= 8, "tile shape");
 
   extern __shared__ __align__(16) unsigned char smem[];
+  // B is staged transposed ([n][k], pitch LDK) with one register set (hw
+  // variant 0), or as loaded ([k][n], pitch PB) and read with the
+  // transposing LDS read (several register sets, hw variant 1).
+  constexpr bool BT = PD > 1;
+  constexpr int PB = bpitch(BN);
   bf16* As = reinterpret_cast<bf16*>(smem);                 // [2][NA][BM][LDK]
-  bf16* Bs = As + 2 * NA * BM * LDK;                        // [2][NB][BN][LDK]
+  bf16* Bs = As + 2 * NA * BM * LDK;                        // [2][NB][BN][LDK] or [2][NB][BK][PB]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -112,42 +135,61 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   // out-of-range elements are zeroed at store time.
   using ARaw = typename std::conditional<A_F32, Vec<float>, Vec<bf16>>::type;
   constexpr int AW = A_F32 ? 2 : 1;  // 16-byte loads per 8 A values
-  ARaw a_raw[AV][AW];
-  bool a_ok[AV];
-  Vec<bf16> b_raw[NB][KR];
-  bool b_ok[KR];
+  // PD register sets; set r holds the loads of the K steps t with t % PD == r.
+  ARaw a_raw[PD][AV][AW];
+  bool a_ok[PD][AV];
+  Vec<bf16> b_raw[PD][NB][KR];
+  bool b_ok[PD][KR];
   float sq[AV];
 #pragma unroll
   for (int j = 0; j < AV; ++j) sq[j] = 0.f;
 
-  auto load_global = [&](int k0) {
+  const int nsteps = (kend - kbeg + BK - 1) / BK;
+  // Loads of steps past this workgroup's K range re-read its last step (L2
+  // hits) and are never stored: they keep the pipeline free of branches, so
+  // the compiler's memory-counter waits stay exact.
+  const int klast = kbeg + max(nsteps - 1, 0) * BK;
+
+  auto load_global = [&](int k0, auto set_tag) {
+    constexpr int P = decltype(set_tag)::value;
+    const int kl = min(k0, klast);
 #pragma unroll
     for (int j = 0; j < AV; ++j) {
       const int v = tid + j * kThreads;
       const int r = v >> 3, kc = (v & 7) * 8;
       const int gm = m0 + r, gk = k0 + kc;
-      a_ok[j] = gm < g.M && gk < kend;
-      const int64_t off = static_cast<int64_t>(min(gm, g.M - 1)) * g.K + min(gk, g.K - 8);
+      a_ok[P][j] = gm < g.M && gk < kend;
+      const int64_t off = static_cast<int64_t>(min(gm, g.M - 1)) * g.K + min(kl + kc, g.K - 8);
       if constexpr (A_F32) {
         const float* src = static_cast<const float*>(g.A) + off;
-        a_raw[j][0] = load_vec(src);
-        a_raw[j][1] = load_vec(src + 4);
+        a_raw[P][j][0] = load_vec(src);
+        a_raw[P][j][1] = load_vec(src + 4);
       } else {
-        a_raw[j][0] = load_vec(static_cast<const bf16*>(g.A) + off);
+        a_raw[P][j][0] = load_vec(static_cast<const bf16*>(g.A) + off);
       }
     }
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
-      const int gk = k0 + b_kb * KR + r;
-      const int gn = n0 + b_nc * 8;
-      b_ok[r] = gk < kend && gn < g.N;
-      const int64_t off = static_cast<int64_t>(min(gk, g.K - 1)) * g.N + min(gn, g.N - 8);
+      // Variant 0: rows b_kb*KR + r of column chunk b_nc. Variant 1: vector
+      // v = tid + r*256 -> row v / (BN/8), chunk v % (BN/8): whole 128-byte
+      // lines per instruction.
+      const int v = tid + r * kThreads;
+      const int kr = BT ? v / (BN / 8) : b_kb * KR + r;
+      const int gn = n0 + (BT ? v % (BN / 8) : b_nc) * 8;
+      const int gk = k0 + kr;
+      b_ok[P][r] = gk < kend && gn < g.N;
+      const int64_t off = static_cast<int64_t>(min(kl + kr, g.K - 1)) * g.N + min(gn, g.N - 8);
 #pragma unroll
-      for (int q = 0; q < NB; ++q) b_raw[q][r] = load_vec((q == 0 ? g.B : g.B2) + off);
+      for (int q = 0; q < NB; ++q) b_raw[P][q][r] = load_vec((q == 0 ? g.B : g.B2) + off);
     }
   };
 
-  auto store_lds = [&](int buf) {
+  auto store_lds = [&](int buf, auto set_tag) {
+    constexpr int P = decltype(set_tag)::value;
+    auto& a_raw_p = a_raw[P];
+    auto& a_ok_p = a_ok[P];
+    auto& b_raw_p = b_raw[P];
+    auto& b_ok_p = b_ok[P];
 #pragma unroll
     for (int j = 0; j < AV; ++j) {
       const int v = tid + j * kThreads;
@@ -156,8 +198,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
       if constexpr (A_F32) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          x[e] = a_ok[j] ? a_raw[j][0].v[e] : 0.f;
-          x[4 + e] = a_ok[j] ? a_raw[j][1].v[e] : 0.f;
+          x[e] = a_ok_p[j] ? a_raw_p[j][0].v[e] : 0.f;
+          x[4 + e] = a_ok_p[j] ? a_raw_p[j][1].v[e] : 0.f;
         }
         Vec<bf16> hi, lo;
 #pragma unroll
@@ -168,8 +210,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         store_vec(As + ((buf * NA + 0) * BM + r) * LDK + kc, hi);
         store_vec(As + ((buf * NA + 1) * BM + r) * LDK + kc, lo);
       } else {
-        Vec<bf16> t = a_raw[j][0];
-        if (!a_ok[j]) {
+        Vec<bf16> t = a_raw_p[j][0];
+        if (!a_ok_p[j]) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) t.v[e] = static_cast<bf16>(0.f);
         }
@@ -184,13 +226,35 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         for (int e = 0; e < 8; ++e) sq[j] += x[e] * x[e];
       }
     }
+    if constexpr (BT) {
+#pragma unroll
+      for (int q = 0; q < NB; ++q)
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+          // Opaque until here: otherwise the zeroing below is placed right
+          // after the load and waits for it PD steps early.
+          u32x4 raw = *reinterpret_cast<const u32x4*>(&b_raw_p[q][r]);
+          asm volatile("" : "+v"(raw));
+          if (!b_ok_p[r]) raw = u32x4{0u, 0u, 0u, 0u};
+          const int v = tid + r * kThreads;
+          *reinterpret_cast<u32x4*>(Bs + ((buf * NB + q) * BK + v / (BN / 8)) * PB + (v % (BN / 8)) * 8) = raw;
+        }
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
       bf16 bv[KR][8];
 #pragma unroll
-      for (int r = 0; r < KR; ++r)
+      for (int r = 0; r < KR; ++r) {
+        // Opaque until here: otherwise the 16-bit extractions below are
+        // placed right after the load and wait for it PD steps early.
+        u32x4 raw = *reinterpret_cast<const u32x4*>(&b_raw_p[q][r]);
+        if constexpr (PD > 1) asm volatile("" : "+v"(raw));
+        Vec<bf16> t;
+        *reinterpret_cast<u32x4*>(&t) = raw;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) bv[r][e] = b_ok[r] ? b_raw[q][r].v[e] : static_cast<bf16>(0.f);
+        for (int e = 0; e < 8; ++e) bv[r][e] = b_ok_p[r] ? t.v[e] : static_cast<bf16>(0.f);
+      }
       bf16* dst = Bs + ((buf * NB + q) * BN + b_nc * 8) * LDK + b_kb * KR;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -227,15 +291,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[q][i][j][e] = 0.f;
 
-  const int nsteps = (kend - kbeg + BK - 1) / BK;
-  if (nsteps > 0) {
-    load_global(kbeg);
-    store_lds(0);
-  }
-  __syncthreads();
-  for (int s = 0; s < nsteps; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < nsteps) load_global(kbeg + (s + 1) * BK);
+  auto compute = [&](int buf) {
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
       const int kof = kk * 16 + (lane >> 5) * 8;
@@ -250,8 +306,24 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
       for (int q = 0; q < NB; ++q) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(
-              Bs + ((buf * NB + q) * BN + wn * WN + j * 32 + (lane & 31)) * LDK + kof);
+          bf16x8 bfr;
+          if constexpr (BT) {
+            // Transposing read: within each 16-lane group, lane i receives
+            // element i%4 of the 4 values lane 4j + i/4 points at, for j =
+            // 0..3. Lane s points at row k0 + s/4, columns nb + 4*(s%4), so
+            // lane i gets k rows k0..k0+3 of column nb + i; a second read
+            // 4 rows down gives k0+4..k0+7 (the MFMA's 8 k values).
+            const int g4 = lane >> 4, s16 = lane & 15;
+            const int nb = wn * WN + j * 32 + 16 * (g4 & 1);
+            const int kr0 = kk * 16 + 8 * (g4 >> 1) + (s16 >> 2);
+            const bf16* bp = Bs + ((buf * NB + q) * BK + kr0) * PB + nb + 4 * (s16 & 3);
+            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp));
+            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp + 4 * PB));
+            bfr = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          } else {
+            bfr = *reinterpret_cast<const bf16x8*>(
+                Bs + ((buf * NB + q) * BN + wn * WN + j * 32 + (lane & 31)) * LDK + kof);
+          }
 #pragma unroll
           for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -261,9 +333,57 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         }
       }
     }
-    if (s + 1 < nsteps) store_lds(buf ^ 1);
-    __syncthreads();
+  };
+
+  // Pipeline: K steps 0..PD-1 are loaded up front; after step s is computed
+  // from LDS buffer s&1, step s+1 moves from its register set into the other
+  // buffer and that set is refilled with step s+1+PD. Full groups of PD steps
+  // run branch-free; the remaining steps run in a short tail.
+  static_assert(PD >= 1 && PD <= 4, "prefetch depth");
+  if (nsteps > 0) {
+    load_global(kbeg, ic<0>{});
+    if constexpr (PD > 1) load_global(kbeg + BK, ic<1>{});
+    if constexpr (PD > 2) load_global(kbeg + 2 * BK, ic<2>{});
+    if constexpr (PD > 3) load_global(kbeg + 3 * BK, ic<3>{});
+    store_lds(0, ic<0>{});
+    load_global(kbeg + PD * BK, ic<0>{});
   }
+  __syncthreads();
+  auto step = [&](int s0, auto j_tag) {
+    constexpr int J = decltype(j_tag)::value;
+    constexpr int NX = (J + 1) % PD;  // register set of step s + 1
+    const int s = s0 + J;
+    compute(s & 1);
+    // Keep the store's data preparation (zeroing, B transposition) after this
+    // step's MFMAs: hoisted, it would wait for register sets still in flight.
+    __builtin_amdgcn_sched_barrier(0);
+    store_lds((s + 1) & 1, ic<NX>{});
+    // The refill reuses the registers the stores just read: issued earlier,
+    // it would need other registers and copies that wait for loads in flight.
+    __builtin_amdgcn_sched_barrier(0);
+    load_global(kbeg + (s + 1 + PD) * BK, ic<NX>{});
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+  };
+  int s0 = 0;
+  for (; s0 + PD <= nsteps; s0 += PD) {
+    step(s0, ic<0>{});
+    if constexpr (PD > 1) step(s0, ic<1>{});
+    if constexpr (PD > 2) step(s0, ic<2>{});
+    if constexpr (PD > 3) step(s0, ic<3>{});
+  }
+  auto tail = [&](auto j_tag) {
+    constexpr int J = decltype(j_tag)::value;
+    constexpr int NX = (J + 1) % PD;
+    const int s = s0 + J;
+    if (s >= nsteps) return;
+    compute(s & 1);
+    if (s + 1 < nsteps) store_lds((s + 1) & 1, ic<NX>{});
+    __syncthreads();
+  };
+  if constexpr (PD > 1) tail(ic<0>{});
+  if constexpr (PD > 2) tail(ic<1>{});
+  if constexpr (PD > 3) tail(ic<2>{});
 
   // ---- row sums of squares (RMSNorm epilogues) ---------------------------
   float* rs_lds = reinterpret_cast<float*>(smem);  // [BM], reuses the A buffers
@@ -432,8 +552,9 @@ bool tile_ok(int tm, int tn) {
   return (tm == 2 || tm == 4 || tm == 8) && (tn == 2 || tn == 4 || tn == 8);
 }
 
-size_t lds_bytes(int BM, int BN, int na, int nb) {
-  return static_cast<size_t>(2) * (na * BM + nb * BN) * LDK * sizeof(bf16);
+size_t lds_bytes(int BM, int BN, int na, int nb, bool btile = false) {
+  const size_t b = btile ? static_cast<size_t>(BK) * bpitch(BN) : static_cast<size_t>(BN) * LDK;
+  return static_cast<size_t>(2) * (na * BM * LDK + nb * b) * sizeof(bf16);
 }
 
 // Dynamic LDS available to one workgroup (160 KiB on gfx950, less the small
@@ -485,11 +606,11 @@ size_t gemm_workspace(int M, int N, int K, int tm, int tn, int tk, int nb) {
   return data_bytes(p, M, N, nb);
 }
 
-template <int BM, int BN, int EPI, bool AF>
+template <int BM, int BN, int EPI, bool AF, int PD>
 void launch_tile(const GemmArgs& g, hipStream_t st) {
   constexpr int na = AF ? 2 : 1, nb = EPI == kSiluMul ? 2 : 1;
-  const size_t lds = lds_bytes(BM, BN, na, nb);
-  auto fn = gemm_kernel<BM, BN, EPI, AF>;
+  const size_t lds = lds_bytes(BM, BN, na, nb, PD > 1);
+  auto fn = gemm_kernel<BM, BN, EPI, AF, PD>;
   // Raising the dynamic LDS limit is idempotent, so a race between threads
   // doing it for the first time is harmless.
   static std::atomic<bool> configured{false};
@@ -507,10 +628,35 @@ void launch_tile(const GemmArgs& g, hipStream_t st) {
   }
 }
 
+// Prefetch depth of hw variant 1 (register sets of loads in flight).
+constexpr int deep_pd(int BM, int BN) { return BM * BN <= 128 * 128 ? 3 : 2; }
+
 template <int EPI, bool AF>
-int dispatch(int BM, int BN, const GemmArgs& g, hipStream_t st) {
+int dispatch(int BM, int BN, const GemmArgs& g, hipStream_t st, int variant = 0) {
+#define AXON_GEMM_CASE(bm, bn)                                           \
+  if (BM == bm && BN == bn) {                                            \
+    if (variant == 1) launch_tile<bm, bn, EPI, AF, deep_pd(bm, bn)>(g, st); \
+    else launch_tile<bm, bn, EPI, AF, 1>(g, st);                         \
+    return launch_status("gemm_kernel");                                 \
+  }
+  AXON_GEMM_CASE(64, 64)
+  AXON_GEMM_CASE(64, 128)
+  AXON_GEMM_CASE(64, 256)
+  AXON_GEMM_CASE(128, 64)
+  AXON_GEMM_CASE(128, 128)
+  AXON_GEMM_CASE(128, 256)
+  AXON_GEMM_CASE(256, 64)
+  AXON_GEMM_CASE(256, 128)
+#undef AXON_GEMM_CASE
+  set_error("no GEMM instantiation for this tile");
+  return AXON_EINVAL;
+}
+
+// silu_mlp keeps one register set (its dual-B stage already holds two).
+template <int EPI, bool AF>
+int dispatch_mlp(int BM, int BN, const GemmArgs& g, hipStream_t st) {
 #define AXON_GEMM_CASE(bm, bn) \
-  if (BM == bm && BN == bn) { launch_tile<bm, bn, EPI, AF>(g, st); return launch_status("gemm_kernel"); }
+  if (BM == bm && BN == bn) { launch_tile<bm, bn, EPI, AF, 1>(g, st); return launch_status("gemm_kernel"); }
   AXON_GEMM_CASE(64, 64)
   AXON_GEMM_CASE(64, 128)
   AXON_GEMM_CASE(64, 256)
@@ -595,12 +741,17 @@ int launch_mm(const Call& c, const void* const* in, void* const* out, void* ws, 
   const Plan p = plan_of(M, N, K, c.tile(0), c.tile(1), c.tile(2));
   const GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[1]), nullptr, out[0], M, N, K, p, ws,
                                1, 1e-6f);
-  return dispatch<EPI, false>(p.BM, p.BN, g, st);
+  return dispatch<EPI, false>(p.BM, p.BN, g, st, c.variant);
 }
 
-const char* summary_mm(int) {
-  return "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, LDS double buffer with B transposed on store, "
-         "split-K with a parallel fixup kernel, XCD-grouped K ranges, fused row-scale epilogue";
+const char* summary_mm(int variant) {
+  return variant == 1
+             ? "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, 2-3 K steps of global loads in flight in "
+               "rotating register sets, LDS double buffer with B transposed on store, split-K with a "
+               "parallel fixup kernel, XCD-grouped K ranges, fused row-scale epilogue"
+             : "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, LDS double buffer with B transposed on "
+               "store, split-K with a parallel fixup kernel, XCD-grouped K ranges, fused row-scale "
+               "epilogue";
 }
 
 // ---- silu_mlp (dims m, n, k, p; x[m,k], w1[k,n], w2[k,n], w3[n,p]) --------
@@ -692,11 +843,11 @@ int launch_mlp(const Call& c, const void* const* in, void* const* out, void* ws,
   void* data = base + L.h;
   const GemmArgs g1 = make_args(in[0], static_cast<const bf16*>(in[1]), static_cast<const bf16*>(in[2]),
                                 H, m, n, k, L.p1, data, 2, 0.f);
-  int rc = dispatch<kSiluMul, false>(L.p1.BM, L.p1.BN, g1, st);
+  int rc = dispatch_mlp<kSiluMul, false>(L.p1.BM, L.p1.BN, g1, st);
   if (rc != AXON_OK) return rc;
   const GemmArgs g2 = make_args(H, static_cast<const bf16*>(in[3]), nullptr, out[0], m, p, n, L.p2,
                                 data, 1, 0.f);
-  return dispatch<kPlain, true>(L.p2.BM, L.p2.BN, g2, st);
+  return dispatch_mlp<kPlain, true>(L.p2.BM, L.p2.BN, g2, st);
 }
 
 const char* summary_mlp(int) {
@@ -708,7 +859,7 @@ const char* summary_mlp(int) {
 
 #define AXON_MM_FAMILY(fn_name, spec_name, EPI)                                                \
   const Family* fn_name() {                                                                  \
-    static const Family f = {spec_name,     1,           2,         1,           3,          \
+    static const Family f = {spec_name,     2,           2,         1,           3,          \
                              kTileArgs3,    3,           summary_mm, manifest_mm, check_mm<EPI>, \
                              workspace_mm<EPI>, outputs_mm, launch_mm<EPI>};                  \
     return &f;                                                                               \

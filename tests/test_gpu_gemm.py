@@ -2,7 +2,8 @@
 
 Every case compares the bf16 output with the fp32 oracle at rtol = atol =
 1e-2 (the bf16 bar), over a diverse selection of legal tile tuples that
-includes split-K (last-arriver reduction) and single-pass schedules, at the
+includes split-K (partials + fixup kernel) and single-pass schedules, in
+both hw variants (one or several K steps of loads in flight), at the
 reference's case shapes, the BASELINE shapes (1024 x 512 x 16384) and ragged
 shapes (m not a multiple of the tile).
 
@@ -44,14 +45,15 @@ def test_gemm_parity(name, sizes):
     assert check_parity(name, sizes, rtol=1e-2, atol=1e-2, budget=10)
 
 
-def test_gemm_repeated_launches_rearm_counters():
-    """Split-K tiles re-arm their counters: ten launches on one workspace give
-    the same bits every time."""
+@pytest.mark.parametrize("variant", [0, 1])
+def test_gemm_repeated_launches_bit_identical(variant):
+    """Split-K launches reuse one workspace: ten launches give the same bits
+    every time (the fixup sums the partials in a fixed order)."""
     from tests._specs import spec_inputs, to_device
 
     spec, dims, host = spec_inputs("matmul_std002", (256, 128, 4096))
     dev = to_device(host)
-    ln = hip.Launcher("matmul_std002", 0, (4, 4, 8), [256, 128, 4096], dev)
+    ln = hip.Launcher("matmul_std002", variant, (4, 4, 8), [256, 128, 4096], dev)
     ln.launch()
     torch.cuda.synchronize()
     first = ln.outputs[0].clone()
