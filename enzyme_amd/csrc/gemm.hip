@@ -349,20 +349,21 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     load_global(kbeg + PD * BK, ic<0>{});
   }
   __syncthreads();
+  // One K step: step s+1 goes from its register set into the buffer computed
+  // on two steps ago (every wave finished reading it before the last
+  // barrier), the set is refilled, and step s is computed while the LDS
+  // absorbs the stores.
   auto step = [&](int s0, auto j_tag) {
     constexpr int J = decltype(j_tag)::value;
     constexpr int NX = (J + 1) % PD;  // register set of step s + 1
     const int s = s0 + J;
-    compute(s & 1);
-    // Keep the store's data preparation (zeroing, B transposition) after this
-    // step's MFMAs: hoisted, it would wait for register sets still in flight.
-    __builtin_amdgcn_sched_barrier(0);
     store_lds((s + 1) & 1, ic<NX>{});
     // The refill reuses the registers the stores just read: issued earlier,
     // it would need other registers and copies that wait for loads in flight.
     __builtin_amdgcn_sched_barrier(0);
     load_global(kbeg + (s + 1 + PD) * BK, ic<NX>{});
     __builtin_amdgcn_sched_barrier(0);
+    compute(s & 1);
     __syncthreads();
   };
   int s0 = 0;
@@ -377,8 +378,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     constexpr int NX = (J + 1) % PD;
     const int s = s0 + J;
     if (s >= nsteps) return;
-    compute(s & 1);
     if (s + 1 < nsteps) store_lds((s + 1) & 1, ic<NX>{});
+    compute(s & 1);
     __syncthreads();
   };
   if constexpr (PD > 1) tail(ic<0>{});
