@@ -134,50 +134,59 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
       for (int i = 0; i < 8; ++i) qf[st][i] = static_cast<bf16>(0.f);
   }
 
-  // Global -> register staging of one K/V block (zeros past the sequence).
+  // Global -> register staging of one K/V block. Rows past the sequence are
+  // read from the last row instead (branch-free loads keep the prefetch in
+  // flight across the block's compute): their scores are masked to -inf and
+  // their probabilities are 0, so the duplicated rows contribute nothing.
   Vec<bf16> kreg[KI][KL], vreg[VI][2];
-  auto zero_vec = [](Vec<bf16>& r) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) r.v[e] = static_cast<bf16>(0.f);
-  };
   auto load_block = [&](int kv0) {
 #pragma unroll
     for (int i = 0; i < KI; ++i) {
-      const int item = tid + i * NT;
-      if (KITEMS % NT != 0 && item >= KITEMS) continue;
+      const int item = min(tid + i * NT, KITEMS - 1);
       if constexpr (!KT) {
         // item -> key item/16, d chunk (item%16)*8
-        const int key = kv0 + (item >> 4), dc = (item & 15) * 8;
-        if (key < a.s) kreg[i][0] = load_vec(K + static_cast<int64_t>(key) * D + dc);
-        else zero_vec(kreg[i][0]);
+        const int key = min(kv0 + (item >> 4), a.s - 1), dc = (item & 15) * 8;
+        kreg[i][0] = load_vec(K + static_cast<int64_t>(key) * D + dc);
       } else {
         // item -> d pair dp = item % 64, key chunk kc = item / 64 (s % 8 == 0)
-        const int dp = item % (D / 2), key = kv0 + (item / (D / 2)) * 8;
+        const int dp = item % (D / 2), key = min(kv0 + (item / (D / 2)) * 8, a.s - 8);
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          if (key < a.s) kreg[i][r] = load_vec(K + static_cast<int64_t>(2 * dp + r) * a.s + key);
-          else zero_vec(kreg[i][r]);
-        }
+        for (int r = 0; r < 2; ++r)
+          kreg[i][r] = load_vec(K + static_cast<int64_t>(2 * dp + r) * a.s + key);
       }
     }
 #pragma unroll
     for (int i = 0; i < VI; ++i) {
-      const int item = tid + i * NT;
-      if (VITEMS % NT != 0 && item >= VITEMS) continue;
+      const int item = min(tid + i * NT, VITEMS - 1);
       // item -> key pair p = item % (BKV/2), d chunk c = item / (BKV/2)
       const int p = item % (BKV / 2), c = item / (BKV / 2);
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        const int key = kv0 + 2 * p + r;
-        if (key < a.s) vreg[i][r] = load_vec(V + static_cast<int64_t>(key) * D + c * 8);
-        else zero_vec(vreg[i][r]);
+        const int key = min(kv0 + 2 * p + r, a.s - 1);
+        vreg[i][r] = load_vec(V + static_cast<int64_t>(key) * D + c * 8);
       }
     }
   };
 
+  // Makes a staged vector opaque until its store: otherwise the packing
+  // below is placed right after the load and waits for it a block early.
+  auto opaque = [](Vec<bf16>& r) {
+    u32x4 u = *reinterpret_cast<const u32x4*>(&r);
+    asm volatile("" : "+v"(u));
+    *reinterpret_cast<u32x4*>(&r) = u;
+  };
   auto store_block = [&](int buf) {
     bf16* ks = Ks + buf * BKV * KP;
     bf16* vt = Vt + buf * D * VP;
+#pragma unroll
+    for (int i = 0; i < KI; ++i)
+#pragma unroll
+      for (int r = 0; r < KL; ++r) opaque(kreg[i][r]);
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      opaque(vreg[i][0]);
+      opaque(vreg[i][1]);
+    }
 #pragma unroll
     for (int i = 0; i < KI; ++i) {
       const int item = tid + i * NT;
