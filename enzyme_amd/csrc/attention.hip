@@ -31,8 +31,13 @@
 // cross the diagonal (or the end of the sequence) are masked, and the
 // heaviest query blocks are scheduled first; the heads are dealt to the 8
 // XCDs so each XCD's L2 serves the K/V of h/8 heads only.
-// Tile arguments: TILES_IN_BLOCK_M = W (waves, 32 queries each),
-//                 TILES_IN_BLOCK_N = BKV / 32; K and P are pinned to 1.
+// With two 32-query tiles per wave (TILES_IN_BLOCK_K = 2) every K and V^T
+// fragment read from LDS feeds two MFMAs, halving LDS reads per FLOP, at one
+// wave per SIMD (the second tile's accumulators fill the AGPRs).
+// Tile arguments: TILES_IN_BLOCK_M = W (waves),
+//                 TILES_IN_BLOCK_N = BKV / 32,
+//                 TILES_IN_BLOCK_K = 32-query tiles per wave (1 or 2);
+//                 TILES_IN_BLOCK_P is pinned to 1.
 #include <atomic>
 #include <type_traits>
 
@@ -75,9 +80,10 @@ __device__ __forceinline__ uint32_t pack2(bf16 lo, bf16 hi) {
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
 }
 
-template <int W, int TN, bool CAUSAL, bool KT>
+template <int W, int TN, int QT, bool CAUSAL, bool KT>
 __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
-  constexpr int BQ = 32 * W;
+  constexpr int QW = 32 * QT;  // queries per wave
+  constexpr int BQ = QW * W;
   constexpr int BKV = 32 * TN;
   constexpr int VP = BKV + 8;  // Vt row pitch (elements)
   constexpr int NT = W * 64;
@@ -119,20 +125,23 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
   bf16* O = a.o + base;
 
   const int q0 = qb * BQ;
-  const int qw = q0 + wave * 32;  // this wave's first query
-  const int my_q = qw + (lane & 31);
+  const int qw = q0 + wave * QW;  // this wave's first query
   const int kv_end = CAUSAL ? min(a.s, q0 + BQ) : a.s;
   const int nblocks = (kv_end + BKV - 1) / BKV;
+  // Query of this lane in query tile u: qw + 32u + lane % 32.
+  auto my_q = [&](int u) { return qw + 32 * u + (lane & 31); };
 
-  // Q^T fragments (B operand): lane holds Q[my_q][step*16 + h*8 .. +8].
-  bf16x8 qf[D / 16];
+  // Q^T fragments (B operand): lane holds Q[my_q(u)][step*16 + h*8 .. +8].
+  bf16x8 qf[QT][D / 16];
 #pragma unroll
-  for (int st = 0; st < D / 16; ++st) {
-    if (my_q < a.s)
-      qf[st] = *reinterpret_cast<const bf16x8*>(Q + static_cast<int64_t>(my_q) * D + st * 16 + h * 8);
-    else
-      for (int i = 0; i < 8; ++i) qf[st][i] = static_cast<bf16>(0.f);
-  }
+  for (int u = 0; u < QT; ++u)
+#pragma unroll
+    for (int st = 0; st < D / 16; ++st) {
+      if (my_q(u) < a.s)
+        qf[u][st] = *reinterpret_cast<const bf16x8*>(Q + static_cast<int64_t>(my_q(u)) * D + st * 16 + h * 8);
+      else
+        for (int i = 0; i < 8; ++i) qf[u][st][i] = static_cast<bf16>(0.f);
+    }
 
   // Global -> register staging of one K/V block. Rows past the sequence are
   // read from the last row instead (branch-free loads keep the prefetch in
@@ -213,65 +222,81 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
     }
   };
 
-  floatx16 acc_o[D / 32];
+  floatx16 acc_o[QT][D / 32];
 #pragma unroll
-  for (int t = 0; t < D / 32; ++t)
+  for (int u = 0; u < QT; ++u)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc_o[t][e] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+    for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc_o[u][t][e] = 0.f;
+  float m_run[QT], l_run[QT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    m_run[u] = -INFINITY;
+    l_run[u] = 0.f;
+  }
 
   // One key block for this wave; MASK applies the causal / sequence-end mask.
+  // Every K and V^T fragment read from LDS feeds the QT query tiles.
   auto process = [&](auto mask_tag, const bf16* ks, const bf16* vt, int kv0) {
     constexpr bool MASK = decltype(mask_tag)::value;
-    // S^T = K Q^T: acc_s[t] rows = keys t*32.., columns = this wave's queries.
-    floatx16 acc_s[TN];
+    // S^T = K Q^T: acc_s[u][t] rows = keys t*32.., columns = query tile u.
+    floatx16 acc_s[QT][TN];
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
+    for (int u = 0; u < QT; ++u)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc_s[t][e] = 0.f;
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_s[u][t][e] = 0.f;
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
 #pragma unroll
       for (int st = 0; st < D / 16; ++st) {
         const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + (t * 32 + (lane & 31)) * KP + st * 16 + h * 8);
-        acc_s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], acc_s[t], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < QT; ++u)
+          acc_s[u][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[u][st], acc_s[u][t], 0, 0, 0);
       }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < TN; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        if constexpr (MASK) {
-          const int key = kv0 + t * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-          if ((CAUSAL && key > my_q) || key >= a.s) acc_s[t][e] = -INFINITY;
-        }
-        mx = fmaxf(mx, acc_s[t][e]);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mxs = mx * a.scale_log2;
-    if (__any(mxs > m_run + kRescaleSlack)) {
-      const float m_new = fmaxf(m_run, mxs);
-      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc_o[dt][e] *= alpha;
-      m_run = m_new;
-    }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    // P^T in bf16, grouped by MFMA k-step: pf[t][ks] holds keys
+    // P^T in bf16, grouped by MFMA k-step: pf[u][t][ks] holds keys
     // t*32 + ks*16 + {0-3, 8-11} (h = 0) or {4-7, 12-15} (h = 1).
-    float lblk = 0.f;
-    bf16x8 pf[TN][2];
+    bf16x8 pf[QT][TN][2];
 #pragma unroll
-    for (int t = 0; t < TN; ++t)
+    for (int u = 0; u < QT; ++u) {
+      float mx = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(acc_s[t][e], a.scale_log2, -m_use));
-        lblk += p;
-        pf[t][e >> 3][e & 7] = static_cast<bf16>(p);
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          if constexpr (MASK) {
+            const int key = kv0 + t * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+            if ((CAUSAL && key > my_q(u)) || key >= a.s) acc_s[u][t][e] = -INFINITY;
+          }
+          mx = fmaxf(mx, acc_s[u][t][e]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mxs = mx * a.scale_log2;
+      if (__any(mxs > m_run[u] + kRescaleSlack)) {
+        const float m_new = fmaxf(m_run[u], mxs);
+        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run[u] - m_new);
+        l_run[u] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc_o[u][dt][e] *= alpha;
+        m_run[u] = m_new;
       }
-    l_run += lblk + __shfl_xor(lblk, 32, 64);
+      const float m_use = m_run[u] == -INFINITY ? 0.f : m_run[u];
+      float lblk = 0.f;
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float pv = __builtin_amdgcn_exp2f(fmaf(acc_s[u][t][e], a.scale_log2, -m_use));
+          lblk += pv;
+          pf[u][t][e >> 3][e & 7] = static_cast<bf16>(pv);
+        }
+      l_run[u] += lblk + __shfl_xor(lblk, 32, 64);
+    }
     // O^T += V^T P^T; the V^T fragment is one 16-byte read (permuted keys).
 #pragma unroll
     for (int t = 0; t < TN; ++t)
@@ -280,7 +305,9 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
           const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vt + (dt * 32 + (lane & 31)) * VP + t * 32 + ks2 * 16 + 8 * h);
-          acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][ks2], acc_o[dt], 0, 0, 0);
+#pragma unroll
+          for (int u = 0; u < QT; ++u)
+            acc_o[u][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[u][t][ks2], acc_o[u][dt], 0, 0, 0);
         }
   };
 
@@ -295,7 +322,7 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
     const int kv0 = blk * BKV;
     if (blk + 1 < nblocks) load_block(kv0 + BKV);
 
-    if ((!CAUSAL || kv0 <= qw + 31) && qw < a.s) {
+    if ((!CAUSAL || kv0 <= qw + QW - 1) && qw < a.s) {
       const bf16* ks = Ks + buf * BKV * KP;
       const bf16* vt = Vt + buf * D * VP;
       const bool mask = (CAUSAL && kv0 + BKV - 1 > qw) || kv0 + BKV > a.s;
@@ -307,17 +334,19 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  if (my_q < a.s) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    if (my_q(u) >= a.s) continue;
+    const float inv = l_run[u] > 0.f ? 1.f / l_run[u] : 0.f;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         bf16x4 out;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) out[i] = static_cast<bf16>(acc_o[dt][g4 * 4 + i] * inv);
+        for (int i = 0; i < 4; ++i) out[i] = static_cast<bf16>(acc_o[u][dt][g4 * 4 + i] * inv);
         const int d = dt * 32 + 8 * g4 + 4 * h;
-        *reinterpret_cast<bf16x4*>(O + static_cast<int64_t>(my_q) * D + d) = out;
+        *reinterpret_cast<bf16x4*>(O + static_cast<int64_t>(my_q(u)) * D + d) = out;
       }
   }
 }
@@ -350,8 +379,12 @@ int check_tiles(const Call& c, std::string* why) {
     *why = "the key block stages more than 8 vectors per thread: need 32*waves >= 8*BKV/8";
     return AXON_EINVAL;
   }
-  if (c.tile(2) != 1 || c.tile(3) != 1) {
-    *why = "TILES_IN_BLOCK_K and TILES_IN_BLOCK_P are unused and must be 1";
+  if (!(c.tile(2) == 1 || c.tile(2) == 2) || c.tile(3) != 1) {
+    *why = "TILES_IN_BLOCK_K (32-query tiles per wave) must be 1 or 2; TILES_IN_BLOCK_P is unused and must be 1";
+    return AXON_EINVAL;
+  }
+  if (c.tile(2) == 2 && (W != 4 || TN > 2)) {
+    *why = "two query tiles per wave fill a SIMD's registers: 4 waves and key blocks of at most 64";
     return AXON_EINVAL;
   }
   return AXON_OK;
@@ -412,7 +445,7 @@ int manifest_attn(int, const int64_t* dims, int, Constraint* out, int cap, int64
   const int64_t sq = s > 0 ? s : 1;
   out[0] = {"TILES_IN_BLOCK_M", 8, 1, false};
   out[1] = {"TILES_IN_BLOCK_N", sq < 128 ? (sq < 32 ? 32 : sq) : 128, 32, false};
-  out[2] = {"TILES_IN_BLOCK_K", 1, 1, false};
+  out[2] = {"TILES_IN_BLOCK_K", 2, 1, false};
   out[3] = {"TILES_IN_BLOCK_P", 1, 1, false};
   return 4;
 }
@@ -437,10 +470,10 @@ void outputs_nki(const int64_t* dims, const int32_t*, OutDesc* out) {
   out[0] = {2, {dims[0], dims[1]}, AXON_BF16};
 }
 
-template <int W, int TN, bool CAUSAL, bool KT>
+template <int W, int TN, int QT, bool CAUSAL, bool KT>
 int launch_t(const AttnArgs& a, hipStream_t st) {
   const size_t lds = attn_lds(TN);
-  auto fn = attn_kernel<W, TN, CAUSAL, KT>;
+  auto fn = attn_kernel<W, TN, QT, CAUSAL, KT>;
   static std::atomic<bool> configured{false};
   if (!configured.load(std::memory_order_acquire)) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -453,13 +486,14 @@ int launch_t(const AttnArgs& a, hipStream_t st) {
 }
 
 template <bool CAUSAL, bool KT>
-int dispatch(int W, int TN, const AttnArgs& a, hipStream_t st) {
-#define AXON_ATTN_CASE(w, tn) \
-  if (W == w && TN == tn) return launch_t<w, tn, CAUSAL, KT>(a, st);
-  AXON_ATTN_CASE(1, 1)
-  AXON_ATTN_CASE(2, 1) AXON_ATTN_CASE(2, 2)
-  AXON_ATTN_CASE(4, 1) AXON_ATTN_CASE(4, 2) AXON_ATTN_CASE(4, 4)
-  AXON_ATTN_CASE(8, 1) AXON_ATTN_CASE(8, 2) AXON_ATTN_CASE(8, 4)
+int dispatch(int W, int TN, int QT, const AttnArgs& a, hipStream_t st) {
+#define AXON_ATTN_CASE(w, tn, qt) \
+  if (W == w && TN == tn && QT == qt) return launch_t<w, tn, qt, CAUSAL, KT>(a, st);
+  AXON_ATTN_CASE(1, 1, 1)
+  AXON_ATTN_CASE(2, 1, 1) AXON_ATTN_CASE(2, 2, 1)
+  AXON_ATTN_CASE(4, 1, 1) AXON_ATTN_CASE(4, 2, 1) AXON_ATTN_CASE(4, 4, 1)
+  AXON_ATTN_CASE(8, 1, 1) AXON_ATTN_CASE(8, 2, 1) AXON_ATTN_CASE(8, 4, 1)
+  AXON_ATTN_CASE(4, 1, 2) AXON_ATTN_CASE(4, 2, 2)
 #undef AXON_ATTN_CASE
   set_error("no attention instantiation for this tile");
   return AXON_EINVAL;
@@ -477,7 +511,7 @@ int launch_common(const Call& c, const void* const* in, void* const* out, hipStr
     set_error("attention output must be 16-byte aligned");
     return AXON_EARG;
   }
-  const int W = c.tile(0), TN = c.tile(1);
+  const int W = c.tile(0), TN = c.tile(1), QT = c.tile(2);
   AttnArgs a;
   a.q = static_cast<const bf16*>(in[0]);
   a.k = static_cast<const bf16*>(in[1]);
@@ -485,7 +519,7 @@ int launch_common(const Call& c, const void* const* in, void* const* out, hipStr
   a.o = static_cast<bf16*>(out[0]);
   a.s = static_cast<int>(s);
   a.bh = static_cast<int>(bh);
-  a.qblocks = static_cast<int>((s + 32 * W - 1) / (32 * W));
+  a.qblocks = static_cast<int>((s + 32 * W * QT - 1) / (32 * W * QT));
   if (static_cast<int64_t>(a.qblocks) * a.bh > (1LL << 31) - 1) {
     set_error("grid too large");
     return AXON_EINVAL;
@@ -494,10 +528,10 @@ int launch_common(const Call& c, const void* const* in, void* const* out, hipStr
   a.xcd_heads = a.bh % kXcds == 0 ? a.bh / kXcds : 0;
   if (causal) {
     a.scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
-    return dispatch<true, false>(W, TN, a, st);
+    return dispatch<true, false>(W, TN, QT, a, st);
   }
   a.scale_log2 = kLog2e;
-  return dispatch<false, true>(W, TN, a, st);
+  return dispatch<false, true>(W, TN, QT, a, st);
 }
 
 int launch_causal(const Call& c, const void* const* in, void* const* out, void*, hipStream_t st) {
