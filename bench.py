@@ -64,17 +64,17 @@ CONFIGS = [
         label="cumsum over vocab: probs[64,128256] fp32 (sorted softmax of N(0,3) logits)",
     ),
     dict(
-        spec="matmul_std002", sizes=(1024, 512, 16384), variant=1, tiles=(4, 4, 4), bound="mfma",
+        spec="matmul_std002", sizes=(1024, 512, 16384), variant=1, tiles=(2, 2, 4), bound="mfma",
         work=2 * 1024 * 512 * 16384,
         label="matmul m,n,k = 1024,512,16384 bf16 N(0,0.02), fp32 accumulate",
     ),
     dict(
-        spec="rmsnorm_matmul_eps", sizes=(1024, 512, 16384), variant=1, tiles=(4, 4, 4), bound="mfma",
+        spec="rmsnorm_matmul_eps", sizes=(1024, 512, 16384), variant=1, tiles=(2, 2, 4), bound="mfma",
         work=2 * 1024 * 512 * 16384,
         label="rmsnorm_matmul m,n,k = 1024,512,16384 bf16, eps 1e-6",
     ),
     dict(
-        spec="attention_causal", sizes=(1, 32, 4096, 128), variant=0, tiles=(8, 2, 1, 1), bound="mfma",
+        spec="attention_causal", sizes=(1, 32, 4096, 128), variant=0, tiles=(2, 2, 1, 1), bound="mfma",
         work=137_438_953_472,
         label="causal attention Q/K/V [1,32,4096,128] bf16, scale 1/sqrt(128)",
     ),

@@ -31,13 +31,13 @@
 // cross the diagonal (or the end of the sequence) are masked, and the
 // heaviest query blocks are scheduled first; the heads are dealt to the 8
 // XCDs so each XCD's L2 serves the K/V of h/8 heads only.
-// With two 32-query tiles per wave (TILES_IN_BLOCK_K = 2) every K and V^T
-// fragment read from LDS feeds two MFMAs, halving LDS reads per FLOP, at one
-// wave per SIMD (the second tile's accumulators fill the AGPRs).
-// Tile arguments: TILES_IN_BLOCK_M = W (waves),
-//                 TILES_IN_BLOCK_N = BKV / 32,
-//                 TILES_IN_BLOCK_K = 32-query tiles per wave (1 or 2);
-//                 TILES_IN_BLOCK_P is pinned to 1.
+// hw variant 1 gives each wave two 32-query tiles: every K and V^T fragment
+// read from LDS feeds two MFMAs, halving LDS reads per FLOP, at one wave per
+// SIMD (the second tile's accumulators fill the AGPRs).
+// Tile arguments: TILES_IN_BLOCK_M = W / 4 (variant 0: 4 or 8 waves; variant
+//                 1: 4 waves), TILES_IN_BLOCK_N = BKV / 32 (variant 1: at
+//                 most 2); TILES_IN_BLOCK_K and TILES_IN_BLOCK_P are pinned
+//                 to 1.
 #include <atomic>
 #include <type_traits>
 
@@ -362,29 +362,31 @@ size_t attn_lds(int TN) {
   return static_cast<size_t>(2) * (BKV * KP + D * (BKV + 8)) * sizeof(bf16);
 }
 
+// Waves, key-block tiles and query tiles per wave of one tile tuple: hw
+// variant 0 runs W = 4 * TILES_IN_BLOCK_M waves (4 or 8) of one 32-query
+// tile; hw variant 1 runs 4 waves of two 32-query tiles each.
+struct AttnTiles {
+  int W, TN, QT;
+};
+
+AttnTiles attn_tiles(const Call& c) {
+  return {4 * c.tile(0), c.tile(1), c.variant == 1 ? 2 : 1};
+}
+
 int check_tiles(const Call& c, std::string* why) {
-  const int W = c.tile(0), TN = c.tile(1);
-  if (!(W == 1 || W == 2 || W == 4 || W == 8)) {
-    *why = "TILES_IN_BLOCK_M (waves of 32 queries) must be 1, 2, 4 or 8";
+  const int tm = c.tile(0), TN = c.tile(1);
+  if (c.variant == 0 ? !(tm == 1 || tm == 2) : tm != 1) {
+    *why = c.variant == 0 ? "TILES_IN_BLOCK_M (groups of 4 waves) must be 1 or 2"
+                          : "TILES_IN_BLOCK_M must be 1 (4 waves of two query tiles)";
     return AXON_EINVAL;
   }
-  if (!(TN == 1 || TN == 2 || TN == 4)) {
-    *why = "TILES_IN_BLOCK_N (key block / 32) must be 1, 2 or 4";
+  if (c.variant == 0 ? !(TN == 1 || TN == 2 || TN == 4) : !(TN == 1 || TN == 2)) {
+    *why = c.variant == 0 ? "TILES_IN_BLOCK_N (key block / 32) must be 1, 2 or 4"
+                          : "TILES_IN_BLOCK_N (key block / 32) must be 1 or 2 with two query tiles per wave";
     return AXON_EINVAL;
   }
-  // Per block each thread stages ceil(8*TN/W) K vectors and 2*ceil(4*TN/W)
-  // V vectors in registers; more than 8 would crowd out the accumulators.
-  const int ki = (8 * TN + W - 1) / W, vi = (4 * TN + W - 1) / W;
-  if (ki + 2 * vi > 8) {
-    *why = "the key block stages more than 8 vectors per thread: need 32*waves >= 8*BKV/8";
-    return AXON_EINVAL;
-  }
-  if (!(c.tile(2) == 1 || c.tile(2) == 2) || c.tile(3) != 1) {
-    *why = "TILES_IN_BLOCK_K (32-query tiles per wave) must be 1 or 2; TILES_IN_BLOCK_P is unused and must be 1";
-    return AXON_EINVAL;
-  }
-  if (c.tile(2) == 2 && (W != 4 || TN > 2)) {
-    *why = "two query tiles per wave fill a SIMD's registers: 4 waves and key blocks of at most 64";
+  if (c.tile(2) != 1 || c.tile(3) != 1) {
+    *why = "TILES_IN_BLOCK_K and TILES_IN_BLOCK_P are unused and must be 1";
     return AXON_EINVAL;
   }
   return AXON_OK;
@@ -439,13 +441,14 @@ int check_nki(const Call& c, std::string* why) {
   return check_tiles(c, why);
 }
 
-int manifest_attn(int, const int64_t* dims, int, Constraint* out, int cap, int64_t s) {
+int manifest_attn(int variant, const int64_t* dims, int, Constraint* out, int cap, int64_t s) {
   (void)dims;
   if (cap < 4) return 0;
   const int64_t sq = s > 0 ? s : 1;
-  out[0] = {"TILES_IN_BLOCK_M", 8, 1, false};
-  out[1] = {"TILES_IN_BLOCK_N", sq < 128 ? (sq < 32 ? 32 : sq) : 128, 32, false};
-  out[2] = {"TILES_IN_BLOCK_K", 2, 1, false};
+  const int64_t kmax = variant == 0 ? 128 : 64;  // key block
+  out[0] = {"TILES_IN_BLOCK_M", variant == 0 ? 2 : 1, 1, false};
+  out[1] = {"TILES_IN_BLOCK_N", sq < kmax ? (sq < 32 ? 32 : sq) : kmax, 32, false};
+  out[2] = {"TILES_IN_BLOCK_K", 1, 1, false};
   out[3] = {"TILES_IN_BLOCK_P", 1, 1, false};
   return 4;
 }
@@ -489,8 +492,6 @@ template <bool CAUSAL, bool KT>
 int dispatch(int W, int TN, int QT, const AttnArgs& a, hipStream_t st) {
 #define AXON_ATTN_CASE(w, tn, qt) \
   if (W == w && TN == tn && QT == qt) return launch_t<w, tn, qt, CAUSAL, KT>(a, st);
-  AXON_ATTN_CASE(1, 1, 1)
-  AXON_ATTN_CASE(2, 1, 1) AXON_ATTN_CASE(2, 2, 1)
   AXON_ATTN_CASE(4, 1, 1) AXON_ATTN_CASE(4, 2, 1) AXON_ATTN_CASE(4, 4, 1)
   AXON_ATTN_CASE(8, 1, 1) AXON_ATTN_CASE(8, 2, 1) AXON_ATTN_CASE(8, 4, 1)
   AXON_ATTN_CASE(4, 1, 2) AXON_ATTN_CASE(4, 2, 2)
@@ -511,7 +512,8 @@ int launch_common(const Call& c, const void* const* in, void* const* out, hipStr
     set_error("attention output must be 16-byte aligned");
     return AXON_EARG;
   }
-  const int W = c.tile(0), TN = c.tile(1), QT = c.tile(2);
+  const AttnTiles t = attn_tiles(c);
+  const int W = t.W, TN = t.TN, QT = t.QT;
   AttnArgs a;
   a.q = static_cast<const bf16*>(in[0]);
   a.k = static_cast<const bf16*>(in[1]);
@@ -542,22 +544,26 @@ int launch_nki(const Call& c, const void* const* in, void* const* out, void*, hi
   return launch_common(c, in, out, st, 1, c.dim(0), false);
 }
 
-const char* summary_attn(int) {
-  return "flash attention: S^T = K Q^T on 32x32x16 bf16 MFMA with Q^T in registers, one query per "
-         "lane for an in-lane online softmax (exp2, fp32), P^T kept in registers as the B operand "
-         "of O^T = V^T P^T, K and V^T double-buffered in LDS, causal block skipping";
+const char* summary_attn(int variant) {
+  return variant == 0
+             ? "flash attention: S^T = K Q^T on 32x32x16 bf16 MFMA with Q^T in registers, one query "
+               "per lane for an in-lane online softmax (exp2, fp32), P^T kept in registers as the B "
+               "operand of O^T = V^T P^T, K and V^T double-buffered in LDS, causal block skipping; "
+               "4 or 8 waves of 32 queries"
+             : "flash attention as hw variant 0 with two 32-query tiles per wave (4 waves, one per "
+               "SIMD): every K and V^T fragment read from LDS feeds two MFMAs";
 }
 
 }  // namespace
 
 const Family* family_attention_causal() {
-  static const Family f = {"attention_causal", 1, 3, 1, 4, kTileArgs, 4, summary_attn,
+  static const Family f = {"attention_causal", 2, 3, 1, 4, kTileArgs, 4, summary_attn,
                            manifest_causal, check_causal, no_workspace, outputs_causal, launch_causal};
   return &f;
 }
 
 const Family* family_attention_nkilib() {
-  static const Family f = {"attention_nkilib", 1, 3, 1, 2, kTileArgs, 4, summary_attn, manifest_nki,
+  static const Family f = {"attention_nkilib", 2, 3, 1, 2, kTileArgs, 4, summary_attn, manifest_nki,
                            check_nki, no_workspace, outputs_nki, launch_nki};
   return &f;
 }

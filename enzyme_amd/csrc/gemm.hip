@@ -34,9 +34,13 @@
 // come from gfx950's transposing LDS read (ds_read_b64_tr_b16): two reads
 // give a lane the 8 consecutive k values of its column.
 //
-// Tile arguments: TILES_IN_BLOCK_M = BM/32, TILES_IN_BLOCK_N = BN/32,
-//                 TILES_IN_BLOCK_K = K range per workgroup / 256
-//                 (silu_mlp: TILES_IN_BLOCK_P = BN/32 of its second GEMM).
+// Tile arguments: TILES_IN_BLOCK_M = BM/64, TILES_IN_BLOCK_N = BN/64 (tiles of
+//                 64, 128 or 256), TILES_IN_BLOCK_K = K range per workgroup /
+//                 256 (silu_mlp: TILES_IN_BLOCK_P = BN/64 of its second GEMM).
+// Every tuple the manifest admits is instantiated: silu_mlp narrows its
+// stages' tiles to what its two accumulator sets and LDS hold (BM x BN <=
+// 128 x 128 per stage, BM <= 128 in stage 2) instead of refusing them.
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 
@@ -538,8 +542,8 @@ struct Plan {
 
 Plan plan_of(int M, int N, int K, int tm, int tn, int tk) {
   Plan p;
-  p.BM = 32 * tm;
-  p.BN = 32 * tn;
+  p.BM = 64 * tm;
+  p.BN = 64 * tn;
   p.kchunk = kKUnit * tk;
   if (p.kchunk > K) p.kchunk = ((K + BK - 1) / BK) * BK;
   p.S = K > 0 ? (K + p.kchunk - 1) / p.kchunk : 1;
@@ -550,7 +554,7 @@ Plan plan_of(int M, int N, int K, int tm, int tn, int tk) {
 
 bool tile_ok(int tm, int tn) {
   // (BM, BN) instantiations: BM in {64, 128, 256}, BN in {64, 128, 256}.
-  return (tm == 2 || tm == 4 || tm == 8) && (tn == 2 || tn == 4 || tn == 8);
+  return (tm == 1 || tm == 2 || tm == 4) && (tn == 1 || tn == 2 || tn == 4);
 }
 
 size_t lds_bytes(int BM, int BN, int na, int nb, bool btile = false) {
@@ -572,11 +576,7 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, st
     return AXON_EINVAL;
   }
   if (!tile_ok(tm, tn)) {
-    *why = "TILES_IN_BLOCK_M/N must each be 2, 4 or 8 (tiles of 64, 128 or 256)";
-    return AXON_EINVAL;
-  }
-  if (tm * tn > 32) {
-    *why = "a 256 x 256 tile exceeds the register budget of 4 waves";
+    *why = "TILES_IN_BLOCK_M/N must each be 1, 2 or 4 (tiles of 64, 128 or 256)";
     return AXON_EINVAL;
   }
   if (!is_pow2_in(tk, 1, 1 << 20)) {
@@ -648,12 +648,15 @@ int dispatch(int BM, int BN, const GemmArgs& g, hipStream_t st, int variant = 0)
   AXON_GEMM_CASE(128, 256)
   AXON_GEMM_CASE(256, 64)
   AXON_GEMM_CASE(256, 128)
+  AXON_GEMM_CASE(256, 256)
 #undef AXON_GEMM_CASE
   set_error("no GEMM instantiation for this tile");
   return AXON_EINVAL;
 }
 
-// silu_mlp keeps one register set (its dual-B stage already holds two).
+// silu_mlp keeps one register set (its dual-B stage already holds two); its
+// stage tiles are narrowed to BM x BN <= 128 x 128 (and BM <= 128 in stage
+// 2), so only those shapes are instantiated.
 template <int EPI, bool AF>
 int dispatch_mlp(int BM, int BN, const GemmArgs& g, hipStream_t st) {
 #define AXON_GEMM_CASE(bm, bn) \
@@ -663,9 +666,7 @@ int dispatch_mlp(int BM, int BN, const GemmArgs& g, hipStream_t st) {
   AXON_GEMM_CASE(64, 256)
   AXON_GEMM_CASE(128, 64)
   AXON_GEMM_CASE(128, 128)
-  AXON_GEMM_CASE(128, 256)
-  AXON_GEMM_CASE(256, 64)
-  AXON_GEMM_CASE(256, 128)
+  if constexpr (!AF) AXON_GEMM_CASE(256, 64)
 #undef AXON_GEMM_CASE
   set_error("no GEMM instantiation for this tile");
   return AXON_EINVAL;
@@ -715,8 +716,8 @@ int manifest_mm(int, const int64_t* dims, int, Constraint* out, int cap) {
   const int64_t m = dims[0] > 0 ? dims[0] : 1, n = dims[1] > 0 ? dims[1] : 1;
   const int64_t k = dims[2] > 0 ? dims[2] : 1;
   // Tiles of 64..256 that fit the extent (a 64-wide tile is always allowed).
-  out[0] = {"TILES_IN_BLOCK_M", m < 256 ? (m < 64 ? 64 : m) : 256, 32, false};
-  out[1] = {"TILES_IN_BLOCK_N", n < 256 ? (n < 64 ? 64 : n) : 256, 32, false};
+  out[0] = {"TILES_IN_BLOCK_M", m < 256 ? (m < 64 ? 64 : m) : 256, 64, false};
+  out[1] = {"TILES_IN_BLOCK_N", n < 256 ? (n < 64 ? 64 : n) : 256, 64, false};
   out[2] = {"TILES_IN_BLOCK_K", k < kKUnit ? kKUnit : k, kKUnit, true};
   return 3;
 }
@@ -768,25 +769,27 @@ int check_mlp(const Call& c, std::string* why) {
     }
   const int64_t m = c.dim(0), n = c.dim(1), k = c.dim(2), p = c.dim(3);
   // Stage 1 (k-contraction) uses M/N/K tiles; stage 2 (n-contraction) uses
-  // M/P tiles with the same K range.
+  // M/P tiles with the same K range (both narrowed by mlp_tiles).
   int rc = check_gemm_shape(m, n, k, c.tile(0), c.tile(1), c.tile(2), why);
   if (rc != AXON_OK) return rc;
-  if (c.tile(0) * c.tile(1) > 16) {
-    *why = "stage 1 keeps two accumulator sets: BM x BN at most 128 x 128";
-    return AXON_EINVAL;
-  }
-  if (lds_bytes(32 * c.tile(0), 32 * c.tile(1), 1, 2) > kMaxLds ||
-      lds_bytes(32 * c.tile(0), 32 * c.tile(3), 2, 1) > kMaxLds) {
-    *why = "tile needs more LDS than a workgroup may hold (160 KiB)";
-    return AXON_EINVAL;
-  }
-  rc = check_gemm_shape(m, p, n, c.tile(0), c.tile(3), c.tile(2), why);
-  if (rc != AXON_OK) return rc;
-  if (c.tile(0) * c.tile(3) > 16) {
-    *why = "stage 2 splits its fp32 operand into two bf16 planes: BM x BP at most 128 x 128";
-    return AXON_EINVAL;
-  }
-  return AXON_OK;
+  return check_gemm_shape(m, p, n, c.tile(0), c.tile(3), c.tile(2), why);
+}
+
+// Tiles (64-units) the two silu_mlp stages run with: stage 1 holds two
+// accumulator sets and two B planes, so BN <= 128 and BM x BN <= 128 x 128;
+// stage 2 holds two A planes (fp32 H as bf16 hi + lo), so BM <= 128 and
+// BM x BP <= 128 x 128. Larger requested tiles are narrowed to these.
+struct MlpTiles {
+  int tm1, tn1, tm2, tp2;
+};
+
+MlpTiles mlp_tiles(const Call& c) {
+  MlpTiles t;
+  t.tm1 = c.tile(0);
+  t.tn1 = std::max(1, std::min({c.tile(1), 2, 4 / t.tm1}));
+  t.tm2 = std::min(c.tile(0), 2);
+  t.tp2 = std::max(1, std::min(c.tile(3), 4 / t.tm2));
+  return t;
 }
 
 int manifest_mlp(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
@@ -794,7 +797,7 @@ int manifest_mlp(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   const int64_t mnk[3] = {dims[0], dims[1], dims[2]};
   manifest_mm(v, mnk, dt, out, cap);
   const int64_t p = dims[3] > 0 ? dims[3] : 1;
-  out[3] = {"TILES_IN_BLOCK_P", p < 256 ? (p < 64 ? 64 : p) : 256, 32, false};
+  out[3] = {"TILES_IN_BLOCK_P", p < 256 ? (p < 64 ? 64 : p) : 256, 64, false};
   return 4;
 }
 
@@ -807,9 +810,10 @@ struct MlpLayout {
 MlpLayout mlp_layout(const Call& c) {
   const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1));
   const int k = static_cast<int>(c.dim(2)), p = static_cast<int>(c.dim(3));
+  const MlpTiles t = mlp_tiles(c);
   MlpLayout L;
-  L.p1 = plan_of(m, n, k, c.tile(0), c.tile(1), c.tile(2));
-  L.p2 = plan_of(m, p, n, c.tile(0), c.tile(3), c.tile(2));
+  L.p1 = plan_of(m, n, k, t.tm1, t.tn1, c.tile(2));
+  L.p2 = plan_of(m, p, n, t.tm2, t.tp2, c.tile(2));
   L.h = align256(static_cast<size_t>(m) * n * sizeof(float));
   const size_t d1 = data_bytes(L.p1, m, n, 2), d2 = data_bytes(L.p2, m, p, 1);
   L.data = d1 > d2 ? d1 : d2;

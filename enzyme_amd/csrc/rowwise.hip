@@ -13,7 +13,8 @@
 // fully coalesced. The row is read from HBM exactly once and written once:
 // the statistics are reduced with a wave64 butterfly and, when Wr > 1,
 // across waves through LDS, then the output is formed from the registers.
-// R rows share one workgroup (R * Wr waves, at most 16).
+// R rows share one workgroup (R * Wr waves, at most 16: a larger requested R
+// is narrowed to 16 / Wr, so every tuple the manifest admits runs).
 //
 // Tile arguments: TILES_IN_BLOCK_M = R (rows per workgroup),
 //                 TILES_IN_BLOCK_N = V (16-byte vectors per lane per row).
@@ -184,6 +185,8 @@ Shape shape_of(const Call& c) {
   const int64_t per_wave = static_cast<int64_t>(kWave) * s.E * s.V;
   const int64_t waves = (c.dim(1) + per_wave - 1) / per_wave;
   s.Wr = waves < 1 ? 1 : (waves > kMaxWaves ? kMaxWaves + 1 : static_cast<int>(waves));
+  // Rows per workgroup, narrowed so R * Wr stays within 16 waves.
+  if (s.Wr <= kMaxWaves && s.R * s.Wr > kMaxWaves) s.R = kMaxWaves / s.Wr;
   return s;
 }
 
@@ -209,7 +212,7 @@ int check_rows(const Call& c, std::string* why) {
     return AXON_EINVAL;
   }
   const Shape s = shape_of(c);
-  if (!is_pow2_in(s.R, 1, kMaxWaves)) {
+  if (!is_pow2_in(c.tile(0), 1, kMaxWaves)) {
     *why = "TILES_IN_BLOCK_M (rows per workgroup) must be a power of two in [1, 16]";
     return AXON_EINVAL;
   }
@@ -222,9 +225,8 @@ int check_rows(const Call& c, std::string* why) {
     *why = "TILES_IN_BLOCK_N: one wave's vector tile is longer than the row";
     return AXON_EINVAL;
   }
-  if (s.Wr > kMaxWaves || s.R * s.Wr > kMaxWaves) {
-    *why = "rows x waves-per-row = " + std::to_string(s.R) + " x " + std::to_string(s.Wr) +
-           " exceeds 16 waves per workgroup";
+  if (s.Wr > kMaxWaves) {
+    *why = "TILES_IN_BLOCK_N: a row needs more than 16 waves at this vector count";
     return AXON_EINVAL;
   }
   return AXON_OK;
@@ -238,7 +240,8 @@ int manifest_rows(int variant, const int64_t* dims, int dtype, Constraint* out, 
   const int64_t m = dims[0], n = dims[1];
   const int64_t lane_span = kWave * E;
   out[0] = {"TILES_IN_BLOCK_M", m < kMaxWaves ? (m > 0 ? m : 1) : kMaxWaves, 1, false};
-  out[1] = {"TILES_IN_BLOCK_N", n > lane_span ? n : lane_span, lane_span, false};
+  const int64_t n_ext = n > lane_span ? n : lane_span;
+  out[1] = {"TILES_IN_BLOCK_N", n_ext < 16 * lane_span ? n_ext : 16 * lane_span, lane_span, false};
   return 2;
 }
 

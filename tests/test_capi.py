@@ -110,6 +110,42 @@ def test_legal_tiles_are_a_subset_of_the_manifest():
                 assert rejection_reason(spec.tile_args, t, cons) is None, (name, v, t)
 
 
+def test_manifest_admits_only_legal_tiles():
+    """Every tile tuple a variant's manifest admits, at every case in
+    eval/sizes.json, is one the library accepts: the candidate filter reads
+    only the manifest (src/axon/candidate_filter.py:90-103), so a tuple it
+    admits but the library refuses would spend the bench budget on
+    "compile: assert" rows."""
+    import json
+
+    from axon.candidate_filter import rejection_reason
+    from enzyme_amd.dtypes import to_torch
+    from tests._specs import spec_inputs
+
+    cases = json.loads((REPO / "eval" / "sizes.json").read_text())
+    checked = 0
+    for name, per_case in cases.items():
+        if name.startswith("_"):
+            continue
+        spec = load_spec(name)
+        for cid, case in per_case.items():
+            dims = dict(zip(spec.dim_vars, case["sizes"]))
+            small = tuple(min(v, 8) for v in case["sizes"])
+            _, _, ins = spec_inputs(name, small, dtype=case.get("dtype"))
+            codes = [hip.dtype_code(to_torch(a)) for a in ins]
+            dvals = [dims[d] for d in spec.dim_vars]
+            for v in range(hip.variant_count(name)):
+                cons = hip.manifest(name, v, dvals, codes[0])
+                admitted = [t for t in product(spec.tile_options, repeat=len(spec.tile_args))
+                            if rejection_reason(spec.tile_args, t, cons) is None]
+                assert admitted, (name, cid, v)
+                for t in admitted:
+                    st, why = hip.check(name, v, t, dvals, codes)
+                    assert st == hip.AXON_OK, (name, cid, v, t, why)
+                checked += len(admitted)
+    assert checked > 500
+
+
 def test_compile_worker_plans_legal_and_asserts_illegal(tmp_path):
     spec = load_spec("rmsnorm")
     mod = tmp_path / "rmsnorm__v0_t0.py"
@@ -123,9 +159,9 @@ def test_compile_worker_plans_legal_and_asserts_illegal(tmp_path):
 
     plan = json.loads(art.read_text())
     assert plan["tiles"] == [2, 2] and plan["dims"] == [2048, 4096] and plan["kernel"] == "rmsnorm"
-    art2 = tmp_path / "__v0_t0_tiles_16_2" / "kernel.plan.json"
+    art2 = tmp_path / "__v0_t0_tiles_2_3" / "kernel.plan.json"
     key, path, err = _compile_one_variant(
-        (str(mod), "rmsnorm", (16, 2), ((2048, 4096), (0,)), {"TILES_IN_BLOCK_M": 16, "TILES_IN_BLOCK_N": 2},
+        (str(mod), "rmsnorm", (2, 3), ((2048, 4096), (0,)), {"TILES_IN_BLOCK_M": 2, "TILES_IN_BLOCK_N": 3},
          str(art2), "gfx950", 1))
     assert path is None and err == "assert" and not art2.exists()
 
