@@ -59,33 +59,38 @@ __global__ __launch_bounds__(1024) void rope_tok_kernel(
     }
   }
 
+  // All H heads' loads are issued before any arithmetic (heads past the last
+  // one re-read the last head and are not stored): with no branch between
+  // them the 2H loads are in flight together.
+  Vec<T> lo[H], hi[H];
+  T* dst[H];
+  bool live[H];
 #pragma unroll
   for (int i = 0; i < H; ++i) {
-    const int h = g + i * HG;
-    if (h >= nh) break;
-    const T* src;
-    T* dst;
-    if (h < hq) {
-      src = q + (t * hq + h) * d;
-      dst = qo + (t * hq + h) * d;
-    } else {
-      src = k + (t * hkv + (h - hq)) * d;
-      dst = ko + (t * hkv + (h - hq)) * d;
-    }
+    const int h0 = g + i * HG;
+    live[i] = h0 < nh;
+    const int h = min(h0, nh - 1);
+    const T* src = h < hq ? q + (t * hq + h) * d : k + (t * hkv + (h - hq)) * d;
+    dst[i] = h < hq ? qo + (t * hq + h) * d : ko + (t * hkv + (h - hq)) * d;
     // q/k are touched exactly once: non-temporal loads and stores stream
     // past the caches (cos/sin above stay cached for the other heads).
-    const Vec<T> lo = load_vec_nt(src + j * E);
-    const Vec<T> hi = load_vec_nt(src + half + j * E);
+    lo[i] = load_vec_nt(src + j * E);
+    hi[i] = load_vec_nt(src + half + j * E);
+  }
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
     Vec<T> olo, ohi;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const float a = to_f32(lo.v[e]);
-      const float b = to_f32(hi.v[e]);
+      const float a = to_f32(lo[i].v[e]);
+      const float b = to_f32(hi[i].v[e]);
       olo.v[e] = from_f32<T>(a * clo[e] - b * slo[e]);
       ohi.v[e] = from_f32<T>(b * chi[e] + a * shi[e]);
     }
-    store_vec_nt(dst + j * E, olo);
-    store_vec_nt(dst + half + j * E, ohi);
+    if (live[i]) {
+      store_vec_nt(dst[i] + j * E, olo);
+      store_vec_nt(dst[i] + half + j * E, ohi);
+    }
   }
 }
 
