@@ -57,6 +57,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.f;  // log2 of the largest un-rescaled probability
 constexpr int kXcds = 8;
 
+template <int N>
+using ic = std::integral_constant<int, N>;
+
 struct AttnArgs {
   const bf16* q;   // [BH][s][D]
   const bf16* k;   // [BH][s][D], or k_t [D][s] when KT
@@ -351,6 +354,264 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
   }
 }
 
+// hw variant 2, software-pipelined: K is staged one block ahead of V, so a
+// wave computes S(j+1) = K(j+1) Q^T on the matrix cores while it runs the
+// softmax of block j on the VALU (the two are independent, and an MFMA keeps
+// running while the same wave issues other instructions), then O += V(j)^T
+// P(j). At the end of iteration j the block's loads land: K(j+2) into the
+// buffer K(j) left (last read in iteration j-1) and V(j+1) into the buffer
+// V(j-1) left; one barrier per block. 4 or 8 waves of 32 queries.
+template <int W, int TN, bool CAUSAL, bool KT>
+__global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
+  constexpr int NT = W * 64;
+  constexpr int BQ = 32 * W;
+  constexpr int BKV = 32 * TN;
+  constexpr int VP = BKV + 8;
+  constexpr int KITEMS = KT ? (D / 2) * (BKV / 8) : BKV * D / 8;
+  constexpr int KI = (KITEMS + NT - 1) / NT;
+  constexpr int VITEMS = (BKV / 2) * (D / 8);
+  constexpr int VI = (VITEMS + NT - 1) / NT;
+  constexpr int KL = KT ? 2 : 1;
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* Ks = reinterpret_cast<bf16*>(smem);  // [2][BKV][KP]
+  bf16* Vt = Ks + 2 * BKV * KP;              // [2][D][VP]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = lane >> 5;
+
+  int rank, bh;
+  const int bid = static_cast<int>(blockIdx.x);
+  if (a.xcd_heads > 0) {
+    const int x = bid % kXcds, j = bid / kXcds;
+    rank = j / a.xcd_heads;
+    bh = x + kXcds * (j % a.xcd_heads);
+  } else {
+    rank = bid % a.qblocks;
+    bh = bid / a.qblocks;
+  }
+  const int qb = CAUSAL ? a.qblocks - 1 - rank : rank;
+  const int64_t base = static_cast<int64_t>(bh) * a.s * D;
+  const bf16* Q = a.q + base;
+  const bf16* K = a.k + base;
+  const bf16* V = a.v + base;
+  bf16* O = a.o + base;
+
+  const int q0 = qb * BQ;
+  const int qw = q0 + wave * 32;
+  const int my_q = qw + (lane & 31);
+  const int kv_end = CAUSAL ? min(a.s, q0 + BQ) : a.s;
+  const int nblocks = (kv_end + BKV - 1) / BKV;
+  const int klast = max(nblocks - 1, 0) * BKV;
+
+  bf16x8 qf[D / 16];
+#pragma unroll
+  for (int st = 0; st < D / 16; ++st) {
+    if (my_q < a.s)
+      qf[st] = *reinterpret_cast<const bf16x8*>(Q + static_cast<int64_t>(my_q) * D + st * 16 + h * 8);
+    else
+      for (int i = 0; i < 8; ++i) qf[st][i] = static_cast<bf16>(0.f);
+  }
+
+  Vec<bf16> kreg[KI][KL], vreg[VI][2];
+  auto opaque = [](Vec<bf16>& r) {
+    u32x4 u = *reinterpret_cast<const u32x4*>(&r);
+    asm volatile("" : "+v"(u));
+    *reinterpret_cast<u32x4*>(&r) = u;
+  };
+  auto load_k = [&](int kv0) {
+    kv0 = min(kv0, klast);
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+      const int item = min(tid + i * NT, KITEMS - 1);
+      if constexpr (!KT) {
+        const int key = min(kv0 + (item >> 4), a.s - 1), dc = (item & 15) * 8;
+        kreg[i][0] = load_vec(K + static_cast<int64_t>(key) * D + dc);
+      } else {
+        const int dp = item % (D / 2), key = min(kv0 + (item / (D / 2)) * 8, a.s - 8);
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+          kreg[i][r] = load_vec(K + static_cast<int64_t>(2 * dp + r) * a.s + key);
+      }
+    }
+  };
+  auto load_v = [&](int kv0) {
+    kv0 = min(kv0, klast);
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      const int item = min(tid + i * NT, VITEMS - 1);
+      const int p = item % (BKV / 2), c = item / (BKV / 2);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int key = min(kv0 + 2 * p + r, a.s - 1);
+        vreg[i][r] = load_vec(V + static_cast<int64_t>(key) * D + c * 8);
+      }
+    }
+  };
+  auto store_k = [&](int buf) {
+    bf16* ks = Ks + buf * BKV * KP;
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+#pragma unroll
+      for (int r = 0; r < KL; ++r) opaque(kreg[i][r]);
+      const int item = tid + i * NT;
+      if (KITEMS % NT != 0 && item >= KITEMS) continue;
+      if constexpr (!KT) {
+        store_vec(ks + (item >> 4) * KP + (item & 15) * 8, kreg[i][0]);
+      } else {
+        const int dp = item % (D / 2), kc = (item / (D / 2)) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          *reinterpret_cast<uint32_t*>(ks + (kc + e) * KP + 2 * dp) = pack2(kreg[i][0].v[e], kreg[i][1].v[e]);
+      }
+    }
+  };
+  auto store_v = [&](int buf) {
+    bf16* vt = Vt + buf * D * VP;
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      opaque(vreg[i][0]);
+      opaque(vreg[i][1]);
+      const int item = tid + i * NT;
+      if (VITEMS % NT != 0 && item >= VITEMS) continue;
+      const int p = item % (BKV / 2), c = item / (BKV / 2);
+      const int k0 = 2 * p;
+      const int pos = (k0 & ~15) | vt_pos(k0 & 15);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<uint32_t*>(vt + (c * 8 + e) * VP + pos) = pack2(vreg[i][0].v[e], vreg[i][1].v[e]);
+    }
+  };
+
+  floatx16 acc_o[D / 32];
+#pragma unroll
+  for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc_o[t][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  floatx16 acc_s[2][TN];  // scores of blocks j (cur) and j+1 (next), by parity
+  bf16x8 pf[TN][2];
+
+  auto m1 = [&](floatx16 (&sacc)[TN], int j) {
+    const bf16* ks = Ks + (j & 1) * BKV * KP;
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[t][e] = 0.f;
+#pragma unroll
+      for (int st = 0; st < D / 16; ++st) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + (t * 32 + (lane & 31)) * KP + st * 16 + h * 8);
+        sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], sacc[t], 0, 0, 0);
+      }
+    }
+  };
+  auto m2 = [&](int j) {
+    const bf16* vt = Vt + (j & 1) * D * VP;
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vt + (dt * 32 + (lane & 31)) * VP + t * 32 + ks2 * 16 + 8 * h);
+          acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][ks2], acc_o[dt], 0, 0, 0);
+        }
+  };
+  // Iteration j (parity P = j & 1): S(j) is in acc_s[P]. The row max and the
+  // (rare) rescale come first; then one branch-free stretch holds the QK^T
+  // MFMAs of block j+1 (into acc_s[P ^ 1]), the exponentials of block j and
+  // its PV MFMAs, so the scheduler can interleave matrix and vector work.
+  // Blocks past a wave's diagonal (or the last block) go through the masked
+  // path and contribute probability 0; S of a block past the end is computed
+  // from a clamped duplicate and never used.
+  auto body = [&](auto mask_tag, auto par_tag, int j) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr int P = decltype(par_tag)::value;
+    floatx16 (&sacc)[TN] = acc_s[P];
+    const int kv0 = j * BKV;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        if constexpr (MASK) {
+          const int key = kv0 + t * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+          if ((CAUSAL && key > my_q) || key >= a.s) sacc[t][e] = -INFINITY;
+        }
+        mx = fmaxf(mx, sacc[t][e]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mxs = mx * a.scale_log2;
+    if (__any(mxs > m_run + kRescaleSlack)) {
+      const float m_new = fmaxf(m_run, mxs);
+      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_o[dt][e] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    m1(acc_s[P ^ 1], j + 1);
+    float lblk = 0.f;
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[t][e], a.scale_log2, -m_use));
+        lblk += pv;
+        pf[t][e >> 3][e & 7] = static_cast<bf16>(pv);
+      }
+    l_run += lblk + __shfl_xor(lblk, 32, 64);
+    m2(j);
+  };
+
+  if (nblocks > 0) {
+    load_k(0);
+    store_k(0);
+    load_k(BKV);
+    load_v(0);
+    store_k(1);
+    store_v(0);
+  }
+  __syncthreads();
+  if (nblocks > 0) m1(acc_s[0], 0);
+
+  auto iter = [&](int j, auto par_tag) {
+    load_k((j + 2) * BKV);
+    load_v((j + 1) * BKV);
+    if (qw < a.s) {
+      const int kv0 = j * BKV;
+      if ((CAUSAL && kv0 + BKV - 1 > qw) || kv0 + BKV > a.s) body(std::true_type{}, par_tag, j);
+      else body(std::false_type{}, par_tag, j);
+    }
+    store_k(j & 1);        // K(j+2) into the buffer K(j) left
+    store_v((j + 1) & 1);  // V(j+1) into the buffer V(j-1) left
+    __syncthreads();
+  };
+  for (int j = 0; j < nblocks; j += 2) {
+    iter(j, ic<0>{});
+    if (j + 1 < nblocks) iter(j + 1, ic<1>{});
+  }
+
+  if (my_q < a.s) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        bf16x4 out;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[i] = static_cast<bf16>(acc_o[dt][g4 * 4 + i] * inv);
+        const int d = dt * 32 + 8 * g4 + 4 * h;
+        *reinterpret_cast<bf16x4*>(O + static_cast<int64_t>(my_q) * D + d) = out;
+      }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -375,8 +636,8 @@ AttnTiles attn_tiles(const Call& c) {
 
 int check_tiles(const Call& c, std::string* why) {
   const int tm = c.tile(0), TN = c.tile(1);
-  if (c.variant == 0 ? !(tm == 1 || tm == 2) : tm != 1) {
-    *why = c.variant == 0 ? "TILES_IN_BLOCK_M (groups of 4 waves) must be 1 or 2"
+  if (c.variant != 1 ? !(tm == 1 || tm == 2) : tm != 1) {
+    *why = c.variant != 1 ? "TILES_IN_BLOCK_M (groups of 4 waves) must be 1 or 2"
                           : "TILES_IN_BLOCK_M must be 1 (4 waves of two query tiles)";
     return AXON_EINVAL;
   }
@@ -445,8 +706,8 @@ int manifest_attn(int variant, const int64_t* dims, int, Constraint* out, int ca
   (void)dims;
   if (cap < 4) return 0;
   const int64_t sq = s > 0 ? s : 1;
-  const int64_t kmax = variant == 0 ? 128 : 64;  // key block
-  out[0] = {"TILES_IN_BLOCK_M", variant == 0 ? 2 : 1, 1, false};
+  const int64_t kmax = variant == 0 ? 128 : 64;  // key block (variants 1, 2: at most 64)
+  out[0] = {"TILES_IN_BLOCK_M", variant == 1 ? 1 : 2, 1, false};
   out[1] = {"TILES_IN_BLOCK_N", sq < kmax ? (sq < 32 ? 32 : sq) : kmax, 32, false};
   out[2] = {"TILES_IN_BLOCK_K", 1, 1, false};
   out[3] = {"TILES_IN_BLOCK_P", 1, 1, false};
@@ -488,8 +749,31 @@ int launch_t(const AttnArgs& a, hipStream_t st) {
   return launch_status("attn_kernel");
 }
 
+template <int W, int TN, bool CAUSAL, bool KT>
+int launch_sp(const AttnArgs& a, hipStream_t st) {
+  const size_t lds = attn_lds(TN);
+  auto fn = attn_sp_kernel<W, TN, CAUSAL, KT>;
+  static std::atomic<bool> configured{false};
+  if (!configured.load(std::memory_order_acquire)) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(lds));
+    configured.store(true, std::memory_order_release);
+  }
+  const unsigned blocks = static_cast<unsigned>(a.qblocks) * static_cast<unsigned>(a.bh);
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(W * 64), lds, st, a);
+  return launch_status("attn_sp_kernel");
+}
+
 template <bool CAUSAL, bool KT>
-int dispatch(int W, int TN, int QT, const AttnArgs& a, hipStream_t st) {
+int dispatch(int W, int TN, int QT, const AttnArgs& a, hipStream_t st, int variant) {
+  if (variant == 2) {
+    if (W == 4 && TN == 1) return launch_sp<4, 1, CAUSAL, KT>(a, st);
+    if (W == 4 && TN == 2) return launch_sp<4, 2, CAUSAL, KT>(a, st);
+    if (W == 8 && TN == 1) return launch_sp<8, 1, CAUSAL, KT>(a, st);
+    if (W == 8 && TN == 2) return launch_sp<8, 2, CAUSAL, KT>(a, st);
+    set_error("no software-pipelined attention instantiation for this tile");
+    return AXON_EINVAL;
+  }
 #define AXON_ATTN_CASE(w, tn, qt) \
   if (W == w && TN == tn && QT == qt) return launch_t<w, tn, qt, CAUSAL, KT>(a, st);
   AXON_ATTN_CASE(4, 1, 1) AXON_ATTN_CASE(4, 2, 1) AXON_ATTN_CASE(4, 4, 1)
@@ -530,10 +814,10 @@ int launch_common(const Call& c, const void* const* in, void* const* out, hipStr
   a.xcd_heads = a.bh % kXcds == 0 ? a.bh / kXcds : 0;
   if (causal) {
     a.scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
-    return dispatch<true, false>(W, TN, QT, a, st);
+    return dispatch<true, false>(W, TN, QT, a, st, c.variant);
   }
   a.scale_log2 = kLog2e;
-  return dispatch<false, true>(W, TN, QT, a, st);
+  return dispatch<false, true>(W, TN, QT, a, st, c.variant);
 }
 
 int launch_causal(const Call& c, const void* const* in, void* const* out, void*, hipStream_t st) {
@@ -550,20 +834,23 @@ const char* summary_attn(int variant) {
                "per lane for an in-lane online softmax (exp2, fp32), P^T kept in registers as the B "
                "operand of O^T = V^T P^T, K and V^T double-buffered in LDS, causal block skipping; "
                "4 or 8 waves of 32 queries"
-             : "flash attention as hw variant 0 with two 32-query tiles per wave (4 waves, one per "
-               "SIMD): every K and V^T fragment read from LDS feeds two MFMAs";
+             : variant == 1
+                   ? "flash attention as hw variant 0 with two 32-query tiles per wave (4 waves, one "
+                     "per SIMD): every K and V^T fragment read from LDS feeds two MFMAs"
+                   : "flash attention as hw variant 0, software-pipelined: K staged a block ahead of "
+                     "V so each wave runs the next block's QK MFMAs under its softmax of this block";
 }
 
 }  // namespace
 
 const Family* family_attention_causal() {
-  static const Family f = {"attention_causal", 2, 3, 1, 4, kTileArgs, 4, summary_attn,
+  static const Family f = {"attention_causal", 3, 3, 1, 4, kTileArgs, 4, summary_attn,
                            manifest_causal, check_causal, no_workspace, outputs_causal, launch_causal};
   return &f;
 }
 
 const Family* family_attention_nkilib() {
-  static const Family f = {"attention_nkilib", 2, 3, 1, 2, kTileArgs, 4, summary_attn, manifest_nki,
+  static const Family f = {"attention_nkilib", 3, 3, 1, 2, kTileArgs, 4, summary_attn, manifest_nki,
                            check_nki, no_workspace, outputs_nki, launch_nki};
   return &f;
 }
