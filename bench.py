@@ -74,7 +74,7 @@ CONFIGS = [
         label="rmsnorm_matmul m,n,k = 1024,512,16384 bf16, eps 1e-6",
     ),
     dict(
-        spec="attention_causal", sizes=(1, 32, 4096, 128), variant=0, tiles=(2, 2, 1, 1), bound="mfma",
+        spec="attention_causal", sizes=(1, 32, 4096, 128), variant=2, tiles=(2, 2, 1, 1), bound="mfma",
         work=137_438_953_472,
         label="causal attention Q/K/V [1,32,4096,128] bf16, scale 1/sqrt(128)",
     ),

@@ -353,6 +353,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     load_global(kbeg + PD * BK, ic<0>{});
   }
   __syncthreads();
+  // Global loads and MFMAs per K step (for the load/MFMA interleave).
+  constexpr int NLOADS = AV * AW + KR * NB;
+  constexpr int NMFMA = (BK / 16) * NB * TM * TN * NA;
+  constexpr int MPL = NMFMA / NLOADS > 0 ? NMFMA / NLOADS : 1;
   // One K step: step s+1 goes from its register set into the buffer computed
   // on two steps ago (every wave finished reading it before the last
   // barrier), the set is refilled, and step s is computed while the LDS
@@ -366,8 +370,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     // it would need other registers and copies that wait for loads in flight.
     __builtin_amdgcn_sched_barrier(0);
     load_global(kbeg + (s + 1 + PD) * BK, ic<NX>{});
-    __builtin_amdgcn_sched_barrier(0);
     compute(s & 1);
+    // Spread the refill's global loads over the step's MFMAs (one load per
+    // two MFMAs) instead of issuing them as one burst the address unit
+    // cannot take in: a wave stalled at a load issues no MFMA either.
+#pragma unroll
+    for (int i = 0; i < NLOADS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one VMEM read
+      __builtin_amdgcn_sched_group_barrier(0x008, MPL, 0);  // MPL MFMAs
+    }
     __syncthreads();
   };
   int s0 = 0;
@@ -458,6 +469,21 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 
   // ---- split K: publish the partial; splitk_reduce_kernel finishes -------
   const int64_t MN = static_cast<int64_t>(g.M) * g.N;
+  if (m0 + BM <= g.M && n0 + BN <= g.N) {
+    // Whole tile in range: no per-element guards.
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      float* dst = g.partial + (static_cast<int64_t>(q) * g.S + z) * MN + static_cast<int64_t>(m0) * g.N + n0;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            dst[static_cast<int64_t>(row_of(i, e)) * g.N + col_of(j)] = acc[q][i][j][e];
+    }
+    return;
+  }
 #pragma unroll
   for (int q = 0; q < NB; ++q)
 #pragma unroll
