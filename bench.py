@@ -64,12 +64,12 @@ CONFIGS = [
         label="cumsum over vocab: probs[64,128256] fp32 (sorted softmax of N(0,3) logits)",
     ),
     dict(
-        spec="matmul_std002", sizes=(1024, 512, 16384), variant=1, tiles=(2, 2, 4), bound="mfma",
+        spec="matmul_std002", sizes=(1024, 512, 16384), variant=1, tiles=(2, 2, 8), bound="mfma",
         work=2 * 1024 * 512 * 16384,
         label="matmul m,n,k = 1024,512,16384 bf16 N(0,0.02), fp32 accumulate",
     ),
     dict(
-        spec="rmsnorm_matmul_eps", sizes=(1024, 512, 16384), variant=1, tiles=(2, 2, 4), bound="mfma",
+        spec="rmsnorm_matmul_eps", sizes=(1024, 512, 16384), variant=1, tiles=(2, 2, 8), bound="mfma",
         work=2 * 1024 * 512 * 16384,
         label="rmsnorm_matmul m,n,k = 1024,512,16384 bf16, eps 1e-6",
     ),

@@ -421,7 +421,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < AV; ++j) {
         const int r = (tid + j * kThreads) >> 3;
-        if ((tid & 7) == 0 && m0 + r < g.M)
+        // Every N tile computes the same row sums; the first one publishes.
+        if ((tid & 7) == 0 && m0 + r < g.M && nt == 0)
           g.rowsq[(static_cast<int64_t>(z) * g.NT + nt) * g.M + m0 + r] = sq[j];
       }
     }
@@ -508,10 +509,28 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) {
   constexpr int NB = EPI == kSiluMul ? 2 : 1;
+  constexpr bool RMS = EPI == kRmsSum || EPI == kRmsEps;
   const int64_t MN = static_cast<int64_t>(g.M) * g.N;
   const int64_t idx = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  const int gm = static_cast<int>(min(idx, MN - 1) / g.N), gn = static_cast<int>(idx - static_cast<int64_t>(gm) * g.N);
+  // RMSNorm epilogues: the row scales of this block's rows (the block's
+  // 1024 outputs span at most 1024 / N + 1 rows, N >= 8) are summed over
+  // the splits once, by one thread per row, instead of by every thread.
+  __shared__ float row_scale[129];
+  if constexpr (RMS) {
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x * 4;
+    const int r0 = static_cast<int>(first / g.N);
+    const int r1 = static_cast<int>(min(first + static_cast<int64_t>(blockDim.x) * 4, MN) - 1) / g.N;
+    const int r = r0 + static_cast<int>(threadIdx.x);
+    if (r <= r1) {
+      const int nt = 0;  // every N tile holds the same row sums; read tile 0's
+      float ss = 0.f;
+      for (int zz = 0; zz < g.S; ++zz) ss += g.rowsq[(static_cast<int64_t>(zz) * g.NT + nt) * g.M + r];
+      row_scale[threadIdx.x] = EPI == kRmsSum ? 1.f / sqrtf(ss) : 1.f / sqrtf(ss / static_cast<float>(g.K) + g.eps);
+    }
+    __syncthreads();
+  }
   if (idx >= MN) return;
-  const int gm = static_cast<int>(idx / g.N), gn = static_cast<int>(idx - static_cast<int64_t>(gm) * g.N);
   float v[NB][4];
 #pragma unroll
   for (int q = 0; q < NB; ++q) {
@@ -535,11 +554,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) 
     for (int e = 0; e < 4; ++e) v[q][e] = t[e];
   }
   float sc = 1.f;
-  if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
-    const int nt = gn / BN;
-    float ss = 0.f;
-    for (int zz = 0; zz < g.S; ++zz) ss += g.rowsq[(static_cast<int64_t>(zz) * g.NT + nt) * g.M + gm];
-    sc = EPI == kRmsSum ? 1.f / sqrtf(ss) : 1.f / sqrtf(ss / static_cast<float>(g.K) + g.eps);
+  if constexpr (RMS) {
+    (void)BN;
+    sc = row_scale[gm - static_cast<int>(static_cast<int64_t>(blockIdx.x) * blockDim.x * 4 / g.N)];
   }
   if constexpr (EPI == kSiluMul) {
     Vec<float> o;
