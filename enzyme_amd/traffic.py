@@ -48,7 +48,7 @@ KERNEL_OF = {
     "cumsum_probs": "scan_",
     "matmul_std002": "gemm_kernel",
     "rmsnorm_matmul_eps": "gemm_kernel",
-    "attention_causal": "attn_kernel",
+    "attention_causal": "attn_",
 }
 
 
