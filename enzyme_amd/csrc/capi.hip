@@ -25,6 +25,7 @@ const Family* family_rmsnorm_matmul_eps();
 const Family* family_silu_mlp();
 const Family* family_attention_causal();
 const Family* family_attention_nkilib();
+const Family* family_qkv_cte();
 
 namespace {
 
@@ -34,6 +35,7 @@ const FamilyFn kFamilyFns[] = {
     family_rope,           family_rope_llama3,        family_fused_adam,    family_cumsum,
     family_cumsum_probs,   family_matmul,             family_matmul_std002, family_rmsnorm_matmul,
     family_rmsnorm_matmul_eps, family_silu_mlp,  family_attention_causal, family_attention_nkilib,
+    family_qkv_cte,
 };
 constexpr int kNumFamilies = sizeof(kFamilyFns) / sizeof(kFamilyFns[0]);
 
@@ -253,6 +255,19 @@ int axon_variant_launch(const char* kernel, int hw_variant, const int32_t* tiles
     set_error(std::string(f->name) + ": expected " + std::to_string(f->n_inputs) + " inputs and " +
               std::to_string(f->n_outputs) + " outputs");
     return AXON_EARG;
+  }
+  // Every output empty: nothing to read or write (empty tensors may carry
+  // null data pointers), so the launch is a no-op.
+  OutDesc d[8];
+  if (f->n_outputs <= 8) {
+    f->outputs(dims, dtypes, d);
+    bool empty = true;
+    for (int i = 0; i < f->n_outputs; ++i) {
+      int64_t e = 1;
+      for (int r = 0; r < d[i].rank; ++r) e *= d[i].shape[r];
+      empty = empty && e == 0;
+    }
+    if (empty) return AXON_OK;
   }
   for (int i = 0; i < n_in; ++i)
     if (inputs[i] == nullptr) {

@@ -1,10 +1,12 @@
 // bf16 MFMA GEMM family: matmul, matmul_std002, rmsnorm_matmul (sum form),
-// rmsnorm_matmul_eps, and the two-stage silu_mlp.
+// rmsnorm_matmul_eps, the two-stage silu_mlp and qkv_cte.
 //
 //   matmul               C = A @ B                         kernels/matmul/kernel.py:7-8
 //   rmsnorm_matmul       C = diag(1/sqrt(sum_k A^2)) (A @ B)  kernels/rmsnorm_matmul/kernel.py:7-16
 //   rmsnorm_matmul_eps   C = diag(rsqrt(mean_k A^2 + 1e-6)) (A @ B)
 //   silu_mlp             H = silu(X @ W1) * (X @ W2);  C = H @ W3  kernels/silu_mlp/kernel.py:7-14
+//   qkv_cte              h = x + mlp_prev + attention_prev;
+//                        C = diag(rsqrt(mean_k h^2 + 1e-6)) (h @ W)   kernels/qkv_cte/kernel.py:18-27
 // A is [M, K] row-major (K contiguous), B is [K, N] row-major (N contiguous),
 // C is [M, N] bf16; accumulation is fp32.
 //
@@ -75,10 +77,12 @@ struct GemmArgs {
   void* C;              // [M, N] bf16, or fp32 H when kSiluMul
   float* partial;       // [S][M][N] fp32 (x2 for kSiluMul)
   float* rowsq;         // [S][NT][M] fp32
+  const float* rscale;  // kPlain: per-row output scale, or null for none
   int M, N, K;
   int kchunk;           // K range per workgroup
   int S, MT, NT;
   float eps;
+  int c_f32;            // kPlain: C is fp32 instead of bf16
 };
 
 __device__ __forceinline__ float silu(float a) { return a / (1.f + __expf(-a)); }
@@ -444,7 +448,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
       static_cast<float*>(g.C)[static_cast<int64_t>(gm) * g.N + gn] = silu(v0) * v1;
     } else {
       (void)v1;
-      static_cast<bf16*>(g.C)[static_cast<int64_t>(gm) * g.N + gn] = static_cast<bf16>(v0);
+      if (EPI == kPlain && g.c_f32) static_cast<float*>(g.C)[static_cast<int64_t>(gm) * g.N + gn] = v0;
+      else static_cast<bf16*>(g.C)[static_cast<int64_t>(gm) * g.N + gn] = static_cast<bf16>(v0);
     }
   };
 
@@ -458,6 +463,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         if (gm >= g.M) continue;
         float sc = 1.f;
         if constexpr (EPI == kRmsSum || EPI == kRmsEps) sc = scale_of(rs_lds[r]);
+        if constexpr (EPI == kPlain) {
+          if (g.rscale != nullptr) sc = g.rscale[gm];
+        }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           const int gn = n0 + col_of(j);
@@ -554,14 +562,20 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) 
     for (int e = 0; e < 4; ++e) v[q][e] = t[e];
   }
   float sc = 1.f;
-  if constexpr (RMS) {
-    (void)BN;
-    sc = row_scale[gm - static_cast<int>(static_cast<int64_t>(blockIdx.x) * blockDim.x * 4 / g.N)];
+  (void)BN;
+  if constexpr (RMS) sc = row_scale[gm - static_cast<int>(static_cast<int64_t>(blockIdx.x) * blockDim.x * 4 / g.N)];
+  if constexpr (EPI == kPlain) {
+    if (g.rscale != nullptr) sc = g.rscale[gm];
   }
   if constexpr (EPI == kSiluMul) {
     Vec<float> o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o.v[e] = silu(v[0][e]) * v[1][e];
+    store_vec(static_cast<float*>(g.C) + idx, o);
+  } else if (EPI == kPlain && g.c_f32) {
+    Vec<float> o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o.v[e] = v[0][e] * sc;
     store_vec(static_cast<float*>(g.C) + idx, o);
   } else {
     typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -570,6 +584,98 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) 
     for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(v[0][e] * sc);
     *reinterpret_cast<bf16x4*>(static_cast<bf16*>(g.C) + idx) = o;
   }
+}
+
+// ---------------------------------------------------------------------------
+// qkv_cte operand preparation (kernels/qkv_cte/kernel.py:22-27): one
+// workgroup per row streams the three residual inputs once, forms
+// h = (x + mlp_prev) + attention_prev in fp32 (the reference's order),
+// accumulates sum h^2 and writes the GEMM's bf16 A operand:
+//   bf16 inputs: A[row] = bf16(h)                          (K' = k)
+//   fp32 inputs: A[row] = [hi(h) | lo(h) | hi(h)]           (K' = 3k)
+// with hi = bf16(h), lo = bf16(h - hi). Paired with B = [hi(w); hi(w); lo(w)]
+// the bf16 GEMM over K' sums hi*hi + lo*hi + hi*lo, leaving only the lo*lo
+// term (about 2^-16 relative) out, so fp32 cases keep fp32-level accuracy.
+// The row scale rsqrt(sum h^2 / k + eps) goes to `rscale`, applied by the
+// GEMM's epilogue; A itself does not depend on it, so no second pass.
+// k % 8 == 0 keeps every 8-element group inside one row and 16-byte aligned.
+// ---------------------------------------------------------------------------
+constexpr int kPrepThreads = 256;
+
+template <typename T>
+__global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const T* __restrict__ x,
+                                                                const T* __restrict__ mp,
+                                                                const T* __restrict__ ap,
+                                                                bf16* __restrict__ a,
+                                                                float* __restrict__ rscale, int k,
+                                                                float eps) {
+  constexpr bool F32 = std::is_same<T, float>::value;
+  const int row = blockIdx.x;
+  const int64_t in_off = static_cast<int64_t>(row) * k;
+  bf16* arow = a + static_cast<int64_t>(row) * (F32 ? 3 * k : k);
+  float ss = 0.f;
+  for (int c = threadIdx.x * 8; c < k; c += kPrepThreads * 8) {
+    float h[8];
+    if constexpr (F32) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const Vec<float> vx = load_vec_nt(x + in_off + c + 4 * half);
+        const Vec<float> vm = load_vec_nt(mp + in_off + c + 4 * half);
+        const Vec<float> va = load_vec_nt(ap + in_off + c + 4 * half);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[4 * half + e] = (vx.v[e] + vm.v[e]) + va.v[e];
+      }
+    } else {
+      const Vec<T> vx = load_vec_nt(x + in_off + c);
+      const Vec<T> vm = load_vec_nt(mp + in_off + c);
+      const Vec<T> va = load_vec_nt(ap + in_off + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[e] = (to_f32(vx.v[e]) + to_f32(vm.v[e])) + to_f32(va.v[e]);
+    }
+    Vec<bf16> hi;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ss += h[e] * h[e];
+      hi.v[e] = static_cast<bf16>(h[e]);
+    }
+    store_vec(arow + c, hi);
+    if constexpr (F32) {
+      Vec<bf16> lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lo.v[e] = static_cast<bf16>(h[e] - static_cast<float>(hi.v[e]));
+      store_vec(arow + k + c, lo);
+      store_vec(arow + 2 * k + c, hi);
+    }
+  }
+  __shared__ float part[kPrepThreads / kWave];
+  ss = wave_sum(ss);
+  if (lane_id() == 0) part[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPrepThreads / kWave; ++i) t += part[i];
+    rscale[row] = 1.f / sqrtf(t * (1.f / static_cast<float>(k)) + eps);
+  }
+}
+
+// B operand of the fp32 qkv_cte GEMM: w [k, n] fp32 -> [hi(w); hi(w); lo(w)],
+// each plane [k, n] bf16. Every thread converts 8 consecutive elements.
+__global__ __launch_bounds__(256) void qkv_split_w_kernel(const float* __restrict__ w,
+                                                         bf16* __restrict__ b, int64_t kn) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  if (i >= kn) return;
+  const Vec<float> v0 = load_vec_nt(w + i), v1 = load_vec_nt(w + i + 4);
+  Vec<bf16> hi, lo;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float f = e < 4 ? v0.v[e] : v1.v[e - 4];
+    hi.v[e] = static_cast<bf16>(f);
+    lo.v[e] = static_cast<bf16>(f - static_cast<float>(hi.v[e]));
+  }
+  store_vec(b + i, hi);
+  store_vec(b + kn + i, hi);
+  store_vec(b + 2 * kn + i, lo);
 }
 
 // ---------------------------------------------------------------------------
@@ -624,6 +730,12 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, st
   }
   if (!is_pow2_in(tk, 1, 1 << 20)) {
     *why = "TILES_IN_BLOCK_K must be a positive power of two";
+    return AXON_EINVAL;
+  }
+  // A K range of at least twice k schedules exactly like the next smaller
+  // power of two: refused, so each legal tuple is a distinct schedule.
+  if (tk > 1 && static_cast<int64_t>(kKUnit / 2) * tk >= K) {
+    *why = "TILES_IN_BLOCK_K covers k twice over; a smaller value gives the same schedule";
     return AXON_EINVAL;
   }
   const Plan p = plan_of(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), tm, tn, tk);
@@ -754,14 +866,23 @@ int check_mm(const Call& c, std::string* why) {
   return check_gemm_shape(c.dim(0), c.dim(1), c.dim(2), c.tile(0), c.tile(1), c.tile(2), why);
 }
 
+// Manifest extent of TILES_IN_BLOCK_K for a contraction of length K: the
+// smallest power-of-two multiple of 256 that covers K. A K range need not
+// divide K (the last one may be ragged), and check_gemm_shape admits exactly
+// the power-of-two ranges up to this extent.
+int64_t k_extent(int64_t K) {
+  int64_t units = (K + kKUnit - 1) / kKUnit, p = 1;
+  while (p < units) p <<= 1;
+  return kKUnit * p;
+}
+
 int manifest_mm(int, const int64_t* dims, int, Constraint* out, int cap) {
   if (cap < 3) return 0;
   const int64_t m = dims[0] > 0 ? dims[0] : 1, n = dims[1] > 0 ? dims[1] : 1;
-  const int64_t k = dims[2] > 0 ? dims[2] : 1;
   // Tiles of 64..256 that fit the extent (a 64-wide tile is always allowed).
   out[0] = {"TILES_IN_BLOCK_M", m < 256 ? (m < 64 ? 64 : m) : 256, 64, false};
   out[1] = {"TILES_IN_BLOCK_N", n < 256 ? (n < 64 ? 64 : n) : 256, 64, false};
-  out[2] = {"TILES_IN_BLOCK_K", k < kKUnit ? kKUnit : k, kKUnit, true};
+  out[2] = {"TILES_IN_BLOCK_K", k_extent(dims[2]), kKUnit, false};
   return 3;
 }
 
@@ -837,7 +958,8 @@ MlpTiles mlp_tiles(const Call& c) {
 
 int manifest_mlp(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   if (cap < 4) return 0;
-  const int64_t mnk[3] = {dims[0], dims[1], dims[2]};
+  // The K range serves both contractions (over k, then over n).
+  const int64_t mnk[3] = {dims[0], dims[1], std::min(dims[1], dims[2])};
   manifest_mm(v, mnk, dt, out, cap);
   const int64_t p = dims[3] > 0 ? dims[3] : 1;
   out[3] = {"TILES_IN_BLOCK_P", p < 256 ? (p < 64 ? 64 : p) : 256, 64, false};
@@ -903,6 +1025,118 @@ const char* summary_mlp(int) {
          "fp32; stage 2: H split into bf16 hi + lo planes (two MFMAs per step) times w3";
 }
 
+// ---- qkv_cte (dims m, n, k; x, mlp_prev, attention_prev [m,k], w [k,n]) --
+// Tiles are the GEMM's over the prepared operands: K' = k (bf16) or 3k (fp32).
+int qkv_kp(int64_t k, int dtype) { return static_cast<int>(dtype == AXON_F32 ? 3 * k : k); }
+
+int check_qkv(const Call& c, std::string* why) {
+  if (c.n_tiles != 3 || c.n_dims != 3 || c.n_dtypes != 4) {
+    *why = "expected 3 tiles, 3 dims (m, n, k) and 4 dtypes";
+    return AXON_EARG;
+  }
+  const int dt = c.dtype(0);
+  if (dt != AXON_BF16 && dt != AXON_F32) {
+    *why = "bf16 or fp32 inputs only";
+    return AXON_EDTYPE;
+  }
+  for (int i = 1; i < 4; ++i)
+    if (c.dtype(i) != dt) {
+      *why = "all four inputs must share one dtype";
+      return AXON_EDTYPE;
+    }
+  if (c.dim(2) > (1 << 28)) {
+    *why = "k out of range";
+    return AXON_EINVAL;
+  }
+  return check_gemm_shape(c.dim(0), c.dim(1), qkv_kp(c.dim(2), dt), c.tile(0), c.tile(1), c.tile(2), why);
+}
+
+int manifest_qkv(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
+  const int64_t mnk[3] = {dims[0], dims[1], dt == AXON_F32 ? 3 * dims[2] : dims[2]};
+  return manifest_mm(v, mnk, dt, out, cap);
+}
+
+struct QkvLayout {
+  Plan p;
+  int kp;
+  size_t scale, a, b, data;  // byte offsets of each region
+  size_t total;
+};
+
+// qkv_cte workspace: [row scales fp32 m][A' bf16 m x K'][B' bf16 K' x n
+// (fp32 inputs only)][split-K data of the GEMM over K'].
+QkvLayout qkv_layout(const Call& c) {
+  const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1));
+  QkvLayout L;
+  L.kp = qkv_kp(c.dim(2), c.dtype(0));
+  L.p = plan_of(m, n, L.kp, c.tile(0), c.tile(1), c.tile(2));
+  L.scale = 0;
+  L.a = align256(static_cast<size_t>(m) * sizeof(float));
+  L.b = L.a + align256(static_cast<size_t>(m) * L.kp * sizeof(bf16));
+  const size_t bbytes = c.dtype(0) == AXON_F32 ? align256(static_cast<size_t>(L.kp) * n * sizeof(bf16)) : 0;
+  L.data = L.b + bbytes;
+  L.total = L.data + data_bytes(L.p, m, n, 1);
+  return L;
+}
+
+size_t workspace_qkv(const Call& c) { return qkv_layout(c).total; }
+
+void outputs_qkv(const int64_t* dims, const int32_t* dtypes, OutDesc* out) {
+  out[0] = {2, {dims[0], dims[1]}, dtypes[0]};
+}
+
+int launch_qkv(const Call& c, const void* const* in, void* const* out, void* ws, hipStream_t st) {
+  const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1)), k = static_cast<int>(c.dim(2));
+  if (m == 0 || n == 0) return AXON_OK;
+  for (int i = 0; i < 4; ++i)
+    if (!aligned16(in[i])) {
+      set_error("qkv_cte buffers must be 16-byte aligned");
+      return AXON_EARG;
+    }
+  if (!aligned16(out[0]) || ws == nullptr) {
+    set_error("qkv_cte needs an aligned output and its workspace");
+    return AXON_EARG;
+  }
+  const bool f32 = c.dtype(0) == AXON_F32;
+  const QkvLayout L = qkv_layout(c);
+  char* base = static_cast<char*>(ws);
+  float* scale = reinterpret_cast<float*>(base + L.scale);
+  bf16* a = reinterpret_cast<bf16*>(base + L.a);
+  const bf16* b = static_cast<const bf16*>(in[3]);
+  const float eps = 1e-6f;
+  if (f32) {
+    hipLaunchKernelGGL(qkv_prep_kernel<float>, dim3(m), dim3(kPrepThreads), 0, st,
+                       static_cast<const float*>(in[0]), static_cast<const float*>(in[1]),
+                       static_cast<const float*>(in[2]), a, scale, k, eps);
+    const int64_t kn = static_cast<int64_t>(k) * n;
+    bf16* bs = reinterpret_cast<bf16*>(base + L.b);
+    if (kn > 0)
+      hipLaunchKernelGGL(qkv_split_w_kernel, dim3(static_cast<unsigned>((kn / 8 + 255) / 256)), dim3(256), 0, st,
+                         static_cast<const float*>(in[3]), bs, kn);
+    b = bs;
+  } else {
+    hipLaunchKernelGGL(qkv_prep_kernel<bf16>, dim3(m), dim3(kPrepThreads), 0, st,
+                       static_cast<const bf16*>(in[0]), static_cast<const bf16*>(in[1]),
+                       static_cast<const bf16*>(in[2]), a, scale, k, eps);
+  }
+  int rc = launch_status("qkv_prep_kernel");
+  if (rc != AXON_OK) return rc;
+  GemmArgs g = make_args(a, b, nullptr, out[0], m, n, L.kp, L.p, base + L.data, 1, eps);
+  g.rscale = scale;
+  g.c_f32 = f32 ? 1 : 0;
+  return dispatch<kPlain, false>(L.p.BM, L.p.BN, g, st, c.variant);
+}
+
+const char* summary_qkv(int variant) {
+  return variant == 1
+             ? "prep: one pass over the three residual inputs writes the bf16 GEMM operand (fp32: "
+               "hi|lo|hi planes, w as hi;hi;lo) and the row scale; GEMM as matmul hw variant 1 with "
+               "the row scale applied in the epilogue"
+             : "prep: one pass over the three residual inputs writes the bf16 GEMM operand (fp32: "
+               "hi|lo|hi planes, w as hi;hi;lo) and the row scale; GEMM as matmul hw variant 0 with "
+               "the row scale applied in the epilogue";
+}
+
 }  // namespace
 
 #define AXON_MM_FAMILY(fn_name, spec_name, EPI)                                                \
@@ -922,6 +1156,12 @@ AXON_MM_FAMILY(family_rmsnorm_matmul_eps, "rmsnorm_matmul_eps", kRmsEps)
 const Family* family_silu_mlp() {
   static const Family f = {"silu_mlp", 1, 4, 1, 4, kTileArgs4, 4, summary_mlp, manifest_mlp,
                            check_mlp, workspace_mlp, outputs_mlp, launch_mlp};
+  return &f;
+}
+
+const Family* family_qkv_cte() {
+  static const Family f = {"qkv_cte", 2, 4, 1, 3, kTileArgs3, 3, summary_qkv, manifest_qkv,
+                           check_qkv, workspace_qkv, outputs_qkv, launch_qkv};
   return &f;
 }
 

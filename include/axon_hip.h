@@ -117,7 +117,9 @@ size_t axon_variant_workspace(const char* kernel, int hw_variant,
                               const int32_t* dtypes, int n_dtypes);
 
 /* Enqueue one launch. Performs the same checks as axon_variant_check plus
- * pointer alignment and workspace size, and enqueues nothing on failure. */
+ * pointer alignment and workspace size, and enqueues nothing on failure.
+ * When every output has zero elements the launch is a no-op that returns
+ * AXON_OK without looking at the pointers (empty buffers may be null). */
 int axon_variant_launch(const char* kernel, int hw_variant,
                         const int32_t* tiles, int n_tiles,
                         const int64_t* dims, int n_dims,

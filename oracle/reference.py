@@ -26,6 +26,7 @@ __all__ = [
     "rmsnorm_matmul_sum",
     "rmsnorm_matmul_eps",
     "silu_mlp",
+    "qkv_cte",
     "attention_nomax",
     "attention_causal",
     "ORACLE",
@@ -161,6 +162,14 @@ def silu_mlp(x, w1, w2, w3):
     return (h1 / (1.0 + torch.exp(-h1)) * (x @ w2)) @ w3
 
 
+def qkv_cte(x, mlp_prev, attention_prev, w, eps=NORM_EPS):
+    """h = (x + mlp_prev) + attention_prev, then (h * rsqrt(mean h^2 + eps)) @ w,
+    in fp32; kernels/qkv_cte/kernel.py:18-27, kernels/qkv_cte/refs.py:30-36."""
+    x, mlp_prev, attention_prev, w = _f32(x, mlp_prev, attention_prev, w)
+    h = (x + mlp_prev) + attention_prev
+    return (h * torch.rsqrt((h * h).mean(dim=-1, keepdim=True) + eps)) @ w
+
+
 def attention_nomax(q, k_t, v):
     """softmax(q @ k_t) @ v with a bare exp/sum softmax;
     kernels/attention_nkilib/refs.py:36-47."""
@@ -204,6 +213,7 @@ ORACLE = {
     "rmsnorm_matmul": rmsnorm_matmul_sum,
     "rmsnorm_matmul_eps": rmsnorm_matmul_eps,
     "silu_mlp": silu_mlp,
+    "qkv_cte": qkv_cte,
     "attention_nkilib": attention_nomax,
     "attention_causal": attention_causal,
 }

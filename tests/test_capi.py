@@ -66,7 +66,7 @@ def test_outputs_match_baseline_shapes(name):
     small = {"rope_llama3": (1, 8, 2, 1, 128), "attention_causal": (1, 2, 16, 128),
              "attention_nkilib": (16, 128), "silu_mlp": (16, 16, 16, 8), "fused_adam": (4, 16),
              "rope": (4, 16), "matmul": (8, 16, 16), "matmul_std002": (8, 16, 16),
-             "rmsnorm_matmul": (8, 16, 16), "rmsnorm_matmul_eps": (8, 16, 16)}
+             "rmsnorm_matmul": (8, 16, 16), "rmsnorm_matmul_eps": (8, 16, 16), "qkv_cte": (8, 16, 16)}
     spec, dims, host = spec_inputs(name, small.get(name, (4, 64)))
     codes = [hip.AXON_BF16 if str(getattr(a, "dtype", "")).endswith("bfloat16") else hip.AXON_F32
              for a in host]
@@ -87,7 +87,8 @@ def test_manifest_literal_reads_back(tmp_path):
     assert cons == tuple(sorted(hip.manifest("matmul_std002", 0, [1024, 512, 16384], hip.AXON_BF16),
                                 key=lambda c: c.tile_arg))
     k = {c.tile_arg: c for c in cons}["TILES_IN_BLOCK_K"]
-    assert k.require_divisible and k.tile_size == 256 and k.extent == 16384
+    # The last K range may be ragged, so the K range need not divide k.
+    assert not k.require_divisible and k.tile_size == 256 and k.extent == 16384
 
 
 def test_legal_tiles_are_a_subset_of_the_manifest():
@@ -96,7 +97,8 @@ def test_legal_tiles_are_a_subset_of_the_manifest():
     from axon.candidate_filter import rejection_reason
 
     cases = {"rmsnorm": [2048, 4096], "cumsum_probs": [64, 128256], "rope_llama3": [1, 4096, 32, 8, 128],
-             "matmul": [1024, 512, 16384], "attention_causal": [1, 32, 4096, 128]}
+             "matmul": [1024, 512, 16384], "attention_causal": [1, 32, 4096, 128],
+             "qkv_cte": [578, 264, 1408]}
     for name, dims in cases.items():
         spec = load_spec(name)
         dt = [hip.AXON_F32] if name == "cumsum_probs" else (

@@ -164,6 +164,23 @@ def pin_silu_mlp(fn):
     assert torch.allclose(fn(x, w1, w2, w3).double(), ref, rtol=1e-5, atol=1e-5)
 
 
+def pin_qkv_cte(fn):
+    # Small magnitudes so eps (1e-6) moves the result by about 10%, and three
+    # different residual streams, so dropping any one of them fails.
+    x, mp, ap = randn(11, 72, scale=1e-3), randn(11, 72, scale=2e-3), randn(11, 72, scale=3e-3)
+    w = randn(72, 9)
+    h = x.double() + mp.double() + ap.double()
+    ref = F.rms_norm(h, (72,), eps=1e-6) @ w.double()
+    assert torch.allclose(fn(x, mp, ap, w).double(), ref, rtol=1e-5, atol=1e-6)
+    # The C restatement: weighted RMSNorm (unit weight, eps 1e-6) of the
+    # summed stream, then the float64 product.
+    cref = clib.matmul_f64(clib.rmsnorm(h.float().numpy(), np.ones(72, np.float32)), w.numpy())
+    assert np.allclose(fn(x, mp, ap, w).numpy(), cref, rtol=1e-5, atol=1e-6)
+    # The row scale is invariant to scaling h when eps is negligible.
+    big = [t * 1e3 for t in (x, mp, ap)]
+    assert torch.allclose(fn(*big, w), fn(*[t * 2e3 for t in (x, mp, ap)], w), rtol=1e-4, atol=1e-5)
+
+
 # ---- attention ------------------------------------------------------------
 def pin_attention_nomax(fn):
     s, d = 40, 16
@@ -198,6 +215,7 @@ PINS = {
     "rmsnorm_matmul_sum": pin_rmsnorm_matmul_sum,
     "rmsnorm_matmul_eps": pin_rmsnorm_matmul_eps,
     "silu_mlp": pin_silu_mlp,
+    "qkv_cte": pin_qkv_cte,
     "attention_nomax": pin_attention_nomax,
     "attention_causal": pin_attention_causal,
 }
@@ -240,6 +258,12 @@ def _mutants():
     def matmul_transposed(x, w):
         return (w.t() @ x.t()).t() * 1.0001
 
+    def qkv_two_residuals(x, mp, ap, w):
+        return oracle.qkv_cte(x, mp, torch.zeros_like(ap), w)
+
+    def qkv_no_eps(x, mp, ap, w):
+        return oracle.qkv_cte(x, mp, ap, w, eps=0.0)
+
     def attn_no_mask(q, k, v):
         return F.scaled_dot_product_attention(q, k, v)
 
@@ -255,6 +279,8 @@ def _mutants():
         ("cumsum", exclusive_cumsum),
         ("fused_adam", adam_no_wd),
         ("matmul", matmul_transposed),
+        ("qkv_cte", qkv_two_residuals),
+        ("qkv_cte", qkv_no_eps),
         ("attention_causal", attn_no_mask),
         ("attention_causal", attn_no_scale),
     ]

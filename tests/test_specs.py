@@ -18,7 +18,7 @@ SMALL = {
     "rope": (4, 16), "rope_llama3": (1, 8, 4, 2, 16), "cumsum": (4, 50), "cumsum_probs": (4, 50),
     "fused_adam": (4, 16), "matmul": (8, 4, 16), "matmul_std002": (8, 4, 16),
     "rmsnorm_matmul": (8, 4, 16), "rmsnorm_matmul_eps": (8, 4, 16), "silu_mlp": (8, 4, 16, 6),
-    "attention_nkilib": (16, 8), "attention_causal": (1, 2, 16, 8),
+    "qkv_cte": (8, 4, 16), "attention_nkilib": (16, 8), "attention_causal": (1, 2, 16, 8),
 }
 
 
@@ -97,3 +97,13 @@ def test_kernelspec_validation():
     with pytest.raises(ValueError, match="duplicate"):
         KernelSpec(name="x", axon_kernel=None, dim_vars=("m", "m"), input_specs=(("x", ("m",)),),
                    make_inputs=None, tile_args=())
+
+
+def test_draw_order_qkv_cte():
+    """x, mlp_prev, attention_prev, then w / sqrt(k), from one generator
+    (kernels/qkv_cte/refs.py:39-48 of the reference)."""
+    _, _, (x, mp, ap, w) = spec_inputs("qkv_cte", (3, 2, 5), dtype="float32")
+    rng = np.random.default_rng(42)
+    want = [rng.standard_normal((3, 5)) for _ in range(3)] + [rng.standard_normal((5, 2)) / np.sqrt(5)]
+    for got, raw in zip((x, mp, ap, w), want):
+        assert np.array_equal(to_f32_numpy(got), raw.astype(np.float32))
