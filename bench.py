@@ -78,6 +78,12 @@ CONFIGS = [
         work=137_438_953_472,
         label="causal attention Q/K/V [1,32,4096,128] bf16, scale 1/sqrt(128)",
     ),
+    dict(
+        spec="qkv_cte", sizes=(16384, 512, 8192), variant=2, tiles=(4, 4, 8), bound="mfma",
+        work=2 * 16384 * 512 * 8192,
+        label="qkv_cte llama70b: x, mlp_prev, attention_prev [16384,8192] bf16 summed, RMSNorm eps 1e-6, "
+              "@ w [8192,512] bf16",
+    ),
 ]
 
 
@@ -282,7 +288,7 @@ def main(argv=None) -> int:
                 row["copy_us"] = round(cu, 3)
                 row["vs_copy"] = round(cu / us, 4)
             if not args.no_cpu:
-                runs = 3 if cfg["spec"] == "attention_causal" else 10
+                runs = 3 if cfg["spec"] in ("attention_causal", "qkv_cte") else 10
                 sec, threads, err, ok = cpu_baseline(cfg, h, o, runs=runs)
                 row["cpu_ms"] = round(sec * 1e3, 3)
                 row["cpu_cores"] = threads

@@ -68,12 +68,19 @@ constexpr int bpitch(int BN) { return BN + 16; }
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;
 
-enum Epi { kPlain = 0, kRmsSum = 1, kRmsEps = 2, kSiluMul = 3 };
+// kQkv: A is the sum of three bf16 inputs (A + A2 + A3, added in fp32 as
+// loaded), with the kRmsEps row scale taken over that sum.
+enum Epi { kPlain = 0, kRmsSum = 1, kRmsEps = 2, kSiluMul = 3, kQkv = 4 };
+
+template <int EPI>
+constexpr bool is_rms() { return EPI == kRmsSum || EPI == kRmsEps || EPI == kQkv; }
 
 struct GemmArgs {
   const void* A;        // [M, K] bf16, or fp32 when A_F32
   const bf16* B;        // [K, N]
   const bf16* B2;       // [K, N] second operand (kSiluMul)
+  const bf16* A2;       // [M, K] second and third addends of A (kQkv)
+  const bf16* A3;
   void* C;              // [M, N] bf16, or fp32 H when kSiluMul
   float* partial;       // [S][M][N] fp32 (x2 for kSiluMul)
   float* rowsq;         // [S][NT][M] fp32
@@ -142,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   // them when the LDS store needs the data, after the current step's MFMAs;
   // out-of-range elements are zeroed at store time.
   using ARaw = typename std::conditional<A_F32, Vec<float>, Vec<bf16>>::type;
-  constexpr int AW = A_F32 ? 2 : 1;  // 16-byte loads per 8 A values
+  constexpr int AW = A_F32 ? 2 : (EPI == kQkv ? 3 : 1);  // 16-byte loads per 8 A values
   // PD register sets; set r holds the loads of the K steps t with t % PD == r.
   ARaw a_raw[PD][AV][AW];
   bool a_ok[PD][AV];
@@ -174,6 +181,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         a_raw[P][j][1] = load_vec(src + 4);
       } else {
         a_raw[P][j][0] = load_vec(static_cast<const bf16*>(g.A) + off);
+        if constexpr (EPI == kQkv) {
+          a_raw[P][j][1] = load_vec(g.A2 + off);
+          a_raw[P][j][2] = load_vec(g.A3 + off);
+        }
       }
     }
 #pragma unroll
@@ -217,6 +228,17 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         }
         store_vec(As + ((buf * NA + 0) * BM + r) * LDK + kc, hi);
         store_vec(As + ((buf * NA + 1) * BM + r) * LDK + kc, lo);
+      } else if constexpr (EPI == kQkv) {
+        // h = (x + mlp_prev) + attention_prev in fp32; its squares feed the
+        // row scale before h is rounded to the bf16 MFMA operand.
+        Vec<bf16> t;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float h = (to_f32(a_raw_p[j][0].v[e]) + to_f32(a_raw_p[j][1].v[e])) + to_f32(a_raw_p[j][2].v[e]);
+          x[e] = a_ok_p[j] ? h : 0.f;
+          t.v[e] = static_cast<bf16>(x[e]);
+        }
+        store_vec(As + ((buf * NA + 0) * BM + r) * LDK + kc, t);
       } else {
         Vec<bf16> t = a_raw_p[j][0];
         if (!a_ok_p[j]) {
@@ -229,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
           for (int e = 0; e < 8; ++e) x[e] = to_f32(t.v[e]);
         }
       }
-      if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
+      if constexpr (is_rms<EPI>()) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) sq[j] += x[e] * x[e];
       }
@@ -407,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 
   // ---- row sums of squares (RMSNorm epilogues) ---------------------------
   float* rs_lds = reinterpret_cast<float*>(smem);  // [BM], reuses the A buffers
-  if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
+  if constexpr (is_rms<EPI>()) {
 #pragma unroll
     for (int j = 0; j < AV; ++j) {
       float v = sq[j];
@@ -439,7 +461,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 
   auto scale_of = [&](float sumsq) -> float {
     if constexpr (EPI == kRmsSum) return 1.f / sqrtf(sumsq);
-    else if constexpr (EPI == kRmsEps) return 1.f / sqrtf(sumsq / static_cast<float>(g.K) + g.eps);
+    else if constexpr (EPI == kRmsEps || EPI == kQkv) return 1.f / sqrtf(sumsq / static_cast<float>(g.K) + g.eps);
     else return 1.f;
   };
 
@@ -462,7 +484,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         const int gm = m0 + r;
         if (gm >= g.M) continue;
         float sc = 1.f;
-        if constexpr (EPI == kRmsSum || EPI == kRmsEps) sc = scale_of(rs_lds[r]);
+        if constexpr (is_rms<EPI>()) sc = scale_of(rs_lds[r]);
         if constexpr (EPI == kPlain) {
           if (g.rscale != nullptr) sc = g.rscale[gm];
         }
@@ -517,7 +539,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) {
   constexpr int NB = EPI == kSiluMul ? 2 : 1;
-  constexpr bool RMS = EPI == kRmsSum || EPI == kRmsEps;
+  constexpr bool RMS = is_rms<EPI>();
   const int64_t MN = static_cast<int64_t>(g.M) * g.N;
   const int64_t idx = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   const int gm = static_cast<int>(min(idx, MN - 1) / g.N), gn = static_cast<int>(idx - static_cast<int64_t>(gm) * g.N);
@@ -827,6 +849,30 @@ int dispatch_mlp(int BM, int BN, const GemmArgs& g, hipStream_t st) {
   return AXON_EINVAL;
 }
 
+// Fused qkv_cte GEMM (kQkv): three A loads per 8 values, so the prefetch
+// depth is 2 up to 128 x 128 tiles and 1 above (register budget).
+constexpr int qkv_pd(int BM, int BN) { return BM * BN <= 128 * 128 ? 2 : 1; }
+
+int dispatch_qkv(int BM, int BN, const GemmArgs& g, hipStream_t st) {
+#define AXON_GEMM_CASE(bm, bn)                                   \
+  if (BM == bm && BN == bn) {                                    \
+    launch_tile<bm, bn, kQkv, false, qkv_pd(bm, bn)>(g, st);     \
+    return launch_status("gemm_kernel");                         \
+  }
+  AXON_GEMM_CASE(64, 64)
+  AXON_GEMM_CASE(64, 128)
+  AXON_GEMM_CASE(64, 256)
+  AXON_GEMM_CASE(128, 64)
+  AXON_GEMM_CASE(128, 128)
+  AXON_GEMM_CASE(128, 256)
+  AXON_GEMM_CASE(256, 64)
+  AXON_GEMM_CASE(256, 128)
+  AXON_GEMM_CASE(256, 256)
+#undef AXON_GEMM_CASE
+  set_error("no GEMM instantiation for this tile");
+  return AXON_EINVAL;
+}
+
 // Fills a GemmArgs for C = A @ B (+ epilogue); `data` is the partial/row-sum
 // region (unused when the plan has S == 1).
 GemmArgs make_args(const void* A, const bf16* B, const bf16* B2, void* C, int M, int N, int K,
@@ -1026,7 +1072,12 @@ const char* summary_mlp(int) {
 }
 
 // ---- qkv_cte (dims m, n, k; x, mlp_prev, attention_prev [m,k], w [k,n]) --
-// Tiles are the GEMM's over the prepared operands: K' = k (bf16) or 3k (fp32).
+// hw variants 0 and 1: a prep pass writes the GEMM operand, then the GEMM of
+// that hw variant runs over K' = k (bf16) or 3k (fp32 hi|lo|hi planes).
+// hw variant 2 (bf16 only): no prep pass; the GEMM's A loads read the three
+// residual inputs and sum them (kQkv), K' = k.
+constexpr int kQkvFused = 2;
+
 int qkv_kp(int64_t k, int dtype) { return static_cast<int>(dtype == AXON_F32 ? 3 * k : k); }
 
 int check_qkv(const Call& c, std::string* why) {
@@ -1044,6 +1095,10 @@ int check_qkv(const Call& c, std::string* why) {
       *why = "all four inputs must share one dtype";
       return AXON_EDTYPE;
     }
+  if (c.variant == kQkvFused && dt != AXON_BF16) {
+    *why = "hw variant 2 sums bf16 residual inputs inside the GEMM; fp32 inputs use hw variants 0 and 1";
+    return AXON_EDTYPE;
+  }
   if (c.dim(2) > (1 << 28)) {
     *why = "k out of range";
     return AXON_EINVAL;
@@ -1053,7 +1108,11 @@ int check_qkv(const Call& c, std::string* why) {
 
 int manifest_qkv(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   const int64_t mnk[3] = {dims[0], dims[1], dt == AXON_F32 ? 3 * dims[2] : dims[2]};
-  return manifest_mm(v, mnk, dt, out, cap);
+  const int n = manifest_mm(v, mnk, dt, out, cap);
+  // The fused variant has no fp32 instantiation: an extent of 0 admits no tile.
+  if (v == kQkvFused && dt != AXON_BF16)
+    for (int i = 0; i < n; ++i) out[i].extent = 0;
+  return n;
 }
 
 struct QkvLayout {
@@ -1071,6 +1130,11 @@ QkvLayout qkv_layout(const Call& c) {
   L.kp = qkv_kp(c.dim(2), c.dtype(0));
   L.p = plan_of(m, n, L.kp, c.tile(0), c.tile(1), c.tile(2));
   L.scale = 0;
+  if (c.variant == kQkvFused) {  // split-K data only
+    L.a = L.b = L.data = 0;
+    L.total = data_bytes(L.p, m, n, 1);
+    return L;
+  }
   L.a = align256(static_cast<size_t>(m) * sizeof(float));
   L.b = L.a + align256(static_cast<size_t>(m) * L.kp * sizeof(bf16));
   const size_t bbytes = c.dtype(0) == AXON_F32 ? align256(static_cast<size_t>(L.kp) * n * sizeof(bf16)) : 0;
@@ -1093,17 +1157,23 @@ int launch_qkv(const Call& c, const void* const* in, void* const* out, void* ws,
       set_error("qkv_cte buffers must be 16-byte aligned");
       return AXON_EARG;
     }
-  if (!aligned16(out[0]) || ws == nullptr) {
+  const QkvLayout L = qkv_layout(c);
+  if (!aligned16(out[0]) || (ws == nullptr && L.total > 0)) {
     set_error("qkv_cte needs an aligned output and its workspace");
     return AXON_EARG;
   }
+  const float eps = 1e-6f;
+  if (c.variant == kQkvFused) {
+    GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[3]), nullptr, out[0], m, n, k, L.p, ws, 1, eps);
+    g.A2 = static_cast<const bf16*>(in[1]);
+    g.A3 = static_cast<const bf16*>(in[2]);
+    return dispatch_qkv(L.p.BM, L.p.BN, g, st);
+  }
   const bool f32 = c.dtype(0) == AXON_F32;
-  const QkvLayout L = qkv_layout(c);
   char* base = static_cast<char*>(ws);
   float* scale = reinterpret_cast<float*>(base + L.scale);
   bf16* a = reinterpret_cast<bf16*>(base + L.a);
   const bf16* b = static_cast<const bf16*>(in[3]);
-  const float eps = 1e-6f;
   if (f32) {
     hipLaunchKernelGGL(qkv_prep_kernel<float>, dim3(m), dim3(kPrepThreads), 0, st,
                        static_cast<const float*>(in[0]), static_cast<const float*>(in[1]),
@@ -1128,6 +1198,10 @@ int launch_qkv(const Call& c, const void* const* in, void* const* out, void* ws,
 }
 
 const char* summary_qkv(int variant) {
+  if (variant == kQkvFused)
+    return "bf16 only: one GEMM whose A loads read x, mlp_prev and attention_prev and add them in "
+           "fp32 (sum of squares taken on the fly, as rmsnorm_matmul_eps), so the residual sum never "
+           "touches HBM; 1-2 K steps of loads in flight, split-K fixup applies the row scale";
   return variant == 1
              ? "prep: one pass over the three residual inputs writes the bf16 GEMM operand (fp32: "
                "hi|lo|hi planes, w as hi;hi;lo) and the row scale; GEMM as matmul hw variant 1 with "
@@ -1160,7 +1234,7 @@ const Family* family_silu_mlp() {
 }
 
 const Family* family_qkv_cte() {
-  static const Family f = {"qkv_cte", 2, 4, 1, 3, kTileArgs3, 3, summary_qkv, manifest_qkv,
+  static const Family f = {"qkv_cte", 3, 4, 1, 3, kTileArgs3, 3, summary_qkv, manifest_qkv,
                            check_qkv, workspace_qkv, outputs_qkv, launch_qkv};
   return &f;
 }

@@ -6,7 +6,8 @@ reference's bf16 case tolerance (rtol 5e-2, atol 1.5e-1, eval/sizes.json);
 fp32 cases to the reference's rtol = atol = 1e-3 (the split-precision GEMM
 keeps about 1e-5). Shapes: the reference's vision_l4 (ragged m = 578,
 n = 264) and llama405b_1k cases in both dtypes, over a diverse selection of
-legal tile tuples in both hw variants (split-K and single-pass schedules),
+legal tile tuples in every hw variant (split-K and single-pass schedules;
+hw variant 2, the fused residual sum, takes bf16 only),
 plus small edge shapes (one row, k = 8, m = 0). The llama70b case
 (16384 x 512 x 8192) is checked against torch's fp32 product on the GPU."""
 
@@ -34,14 +35,20 @@ def test_qkv_bf16_reference_cases(sizes):
 
 @pytest.mark.parametrize("sizes", [(578, 264, 1408), (1024, 512, 16384)], ids=["vision_l4", "llama405b_1k"])
 def test_qkv_fp32_reference_cases(sizes):
-    assert check_parity("qkv_cte", sizes, rtol=1e-3, atol=1e-3, budget=6, dtype="float32")
+    assert check_parity("qkv_cte", sizes, rtol=1e-3, atol=1e-3, budget=6, dtype="float32", variants=(0, 1))
 
 
 @pytest.mark.parametrize("dtype", [None, "float32"], ids=["bf16", "fp32"])
 @pytest.mark.parametrize("sizes", [(1, 8, 8), (77, 136, 520), (130, 72, 64)])
 def test_qkv_edge_shapes(sizes, dtype):
     tol = 1e-3 if dtype == "float32" else 2e-2
-    assert check_parity("qkv_cte", sizes, rtol=tol, atol=tol, dtype=dtype, budget=4)
+    variants = (0, 1) if dtype == "float32" else None
+    assert check_parity("qkv_cte", sizes, rtol=tol, atol=tol, dtype=dtype, budget=4, variants=variants)
+
+
+def test_qkv_fused_variant_refuses_fp32():
+    st, why = hip.check("qkv_cte", 2, (2, 2, 4), [256, 128, 4096], [hip.AXON_F32] * 4)
+    assert st == hip.AXON_EDTYPE and "bf16" in why
 
 
 def test_qkv_zero_rows_is_a_no_op():
@@ -56,7 +63,7 @@ def test_qkv_zero_rows_is_a_no_op():
     assert torch.all(out == 7.0)
 
 
-@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("variant", [0, 1, 2])
 def test_qkv_llama70b_against_torch_fp32(variant):
     """Full llama70b shape (16384 x 512 x 8192, bf16 inputs), split-K tiles:
     compared with torch's fp32 restatement of the reference formula on the
@@ -73,14 +80,15 @@ def test_qkv_llama70b_against_torch_fp32(variant):
     torch.testing.assert_close(ln.outputs[0].float(), ref, rtol=2e-2, atol=2e-2)
 
 
-@pytest.mark.parametrize("dtype", [None, "float32"], ids=["bf16", "fp32"])
-def test_qkv_repeated_launches_bit_identical(dtype):
+@pytest.mark.parametrize(("dtype", "variant"), [(None, 1), (None, 2), ("float32", 1)],
+                         ids=["bf16-v1", "bf16-v2", "fp32-v1"])
+def test_qkv_repeated_launches_bit_identical(dtype, variant):
     """Split-K sums its partials in a fixed order and the prep pass is
     elementwise, so relaunching over the same workspace reproduces the
     output bit for bit."""
     spec, dims, host = spec_inputs("qkv_cte", (256, 128, 4096), dtype=dtype)
     dev = to_device(host)
-    ln = hip.Launcher("qkv_cte", 1, (2, 2, 4), [256, 128, 4096], dev)
+    ln = hip.Launcher("qkv_cte", variant, (2, 2, 4), [256, 128, 4096], dev)
     ln.launch()
     torch.cuda.synchronize()
     first = ln.outputs[0].clone()
