@@ -26,6 +26,9 @@ const Family* family_silu_mlp();
 const Family* family_attention_causal();
 const Family* family_attention_nkilib();
 const Family* family_qkv_cte();
+const Family* family_softmax_mm();
+const Family* family_linear_attention();
+const Family* family_attention_qkv();
 
 namespace {
 
@@ -35,7 +38,7 @@ const FamilyFn kFamilyFns[] = {
     family_rope,           family_rope_llama3,        family_fused_adam,    family_cumsum,
     family_cumsum_probs,   family_matmul,             family_matmul_std002, family_rmsnorm_matmul,
     family_rmsnorm_matmul_eps, family_silu_mlp,  family_attention_causal, family_attention_nkilib,
-    family_qkv_cte,
+    family_qkv_cte,        family_softmax_mm,         family_linear_attention, family_attention_qkv,
 };
 constexpr int kNumFamilies = sizeof(kFamilyFns) / sizeof(kFamilyFns[0]);
 

@@ -70,10 +70,15 @@ constexpr int kXcds = 8;
 
 // kQkv: A is the sum of three bf16 inputs (A + A2 + A3, added in fp32 as
 // loaded), with the kRmsEps row scale taken over that sum.
-enum Epi { kPlain = 0, kRmsSum = 1, kRmsEps = 2, kSiluMul = 3, kQkv = 4 };
+// kSoftmax: A is replaced by exp(A) as loaded (fp32), and the output row is
+// scaled by 1 / sum_k exp(A): softmax without max subtraction, then @ B.
+enum Epi { kPlain = 0, kRmsSum = 1, kRmsEps = 2, kSiluMul = 3, kQkv = 4, kSoftmax = 5 };
 
+// Epilogues that scale each output row by a statistic of its A row, summed
+// over K as the A tiles are staged (squares for the RMS forms, the values
+// themselves for kSoftmax).
 template <int EPI>
-constexpr bool is_rms() { return EPI == kRmsSum || EPI == kRmsEps || EPI == kQkv; }
+constexpr bool is_rms() { return EPI == kRmsSum || EPI == kRmsEps || EPI == kQkv || EPI == kSoftmax; }
 
 struct GemmArgs {
   const void* A;        // [M, K] bf16, or fp32 when A_F32
@@ -220,6 +225,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
           x[e] = a_ok_p[j] ? a_raw_p[j][0].v[e] : 0.f;
           x[4 + e] = a_ok_p[j] ? a_raw_p[j][1].v[e] : 0.f;
         }
+        if constexpr (EPI == kSoftmax) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = a_ok_p[j] ? __expf(x[e]) : 0.f;
+        }
         Vec<bf16> hi, lo;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -239,6 +248,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
           t.v[e] = static_cast<bf16>(x[e]);
         }
         store_vec(As + ((buf * NA + 0) * BM + r) * LDK + kc, t);
+      } else if constexpr (EPI == kSoftmax) {
+        // exp in fp32; the row sum takes the unrounded values.
+        Vec<bf16> t;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          x[e] = a_ok_p[j] ? __expf(to_f32(a_raw_p[j][0].v[e])) : 0.f;
+          t.v[e] = static_cast<bf16>(x[e]);
+        }
+        store_vec(As + ((buf * NA + 0) * BM + r) * LDK + kc, t);
       } else {
         Vec<bf16> t = a_raw_p[j][0];
         if (!a_ok_p[j]) {
@@ -251,7 +269,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
           for (int e = 0; e < 8; ++e) x[e] = to_f32(t.v[e]);
         }
       }
-      if constexpr (is_rms<EPI>()) {
+      if constexpr (EPI == kSoftmax) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sq[j] += x[e];
+      } else if constexpr (is_rms<EPI>()) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) sq[j] += x[e] * x[e];
       }
@@ -461,6 +482,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 
   auto scale_of = [&](float sumsq) -> float {
     if constexpr (EPI == kRmsSum) return 1.f / sqrtf(sumsq);
+    else if constexpr (EPI == kSoftmax) return 1.f / sumsq;
     else if constexpr (EPI == kRmsEps || EPI == kQkv) return 1.f / sqrtf(sumsq / static_cast<float>(g.K) + g.eps);
     else return 1.f;
   };
@@ -556,7 +578,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) 
       const int nt = 0;  // every N tile holds the same row sums; read tile 0's
       float ss = 0.f;
       for (int zz = 0; zz < g.S; ++zz) ss += g.rowsq[(static_cast<int64_t>(zz) * g.NT + nt) * g.M + r];
-      row_scale[threadIdx.x] = EPI == kRmsSum ? 1.f / sqrtf(ss) : 1.f / sqrtf(ss / static_cast<float>(g.K) + g.eps);
+      row_scale[threadIdx.x] = EPI == kRmsSum    ? 1.f / sqrtf(ss)
+                               : EPI == kSoftmax ? 1.f / ss
+                                                 : 1.f / sqrtf(ss / static_cast<float>(g.K) + g.eps);
     }
     __syncthreads();
   }
@@ -1211,6 +1235,285 @@ const char* summary_qkv(int variant) {
                "the row scale applied in the epilogue";
 }
 
+// ---- transposes between GEMM stages ---------------------------------------
+// out[c][r] = in[r][c] for a [R, C] bf16 matrix, through a 64 x 64 LDS tile
+// (row pitch 66 elements: the column reads of one wave touch distinct banks).
+constexpr int kTp = 64;
+
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const bf16* __restrict__ in,
+                                                            bf16* __restrict__ out, int R, int C) {
+  __shared__ bf16 tile[kTp][kTp + 2];
+  const int r0 = blockIdx.y * kTp, c0 = blockIdx.x * kTp;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < kTp; i += 4) {
+    const int r = r0 + ty + i, c = c0 + tx;
+    tile[ty + i][tx] = (r < R && c < C) ? in[static_cast<int64_t>(r) * C + c] : static_cast<bf16>(0.f);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kTp; i += 4) {
+    const int c = c0 + ty + i, r = r0 + tx;
+    if (c < C && r < R) out[static_cast<int64_t>(c) * R + r] = tile[tx][ty + i];
+  }
+}
+
+int launch_transpose(const bf16* in, bf16* out, int R, int C, hipStream_t st) {
+  if (R == 0 || C == 0) return AXON_OK;
+  const dim3 grid((C + kTp - 1) / kTp, (R + kTp - 1) / kTp);
+  hipLaunchKernelGGL(transpose_bf16_kernel, grid, dim3(256), 0, st, in, out, R, C);
+  return launch_status("transpose_bf16_kernel");
+}
+
+int check_all_bf16(const Call& c, int n, std::string* why) {
+  for (int i = 0; i < n; ++i)
+    if (c.dtype(i) != AXON_BF16) {
+      *why = "bf16 inputs only";
+      return AXON_EDTYPE;
+    }
+  return AXON_OK;
+}
+
+// ---- softmax_mm (dims m, n, k; x [m,k], w [k,n]) ---------------------------
+// One GEMM (kSoftmax): exp(x) formed as the A tiles are staged, the row sums
+// of exp(x) taken on the fly, the output row scaled by 1 / sum in the
+// epilogue (or in the split-K fixup). kernels/softmax_mm/kernel.py:7-11.
+const char* summary_softmax_mm(int variant) {
+  return variant == 1
+             ? "one bf16 MFMA GEMM (hw variant 1 schedule) with exp applied to A as it is staged, "
+               "row sums of exp taken on the fly and 1/sum applied in the epilogue"
+             : "one bf16 MFMA GEMM (hw variant 0 schedule) with exp applied to A as it is staged, "
+               "row sums of exp taken on the fly and 1/sum applied in the epilogue";
+}
+
+// ---- linear_attention (dims sq, sk, dk, dv; q [sq,dk], key [sk,dk], v [sk,dv])
+// out = q (keyᵀ v) (kernels/linear_attention/kernel.py:16-27): key is
+// transposed into the workspace, state = keyᵀ v is a split-K GEMM over sk
+// (bf16 state, fp32 accumulation), then out = q state over dk.
+// Tiles: TILES_IN_BLOCK_P = state rows per tile / 64 (over dk),
+// TILES_IN_BLOCK_N = columns per tile / 64 (over dv, both GEMMs),
+// TILES_IN_BLOCK_K = state K range / 256 (over sk),
+// TILES_IN_BLOCK_M = output rows per tile / 64 (over sq); the output GEMM
+// contracts the whole dk in one K range.
+int la_tk2(int64_t dk) { return static_cast<int>(k_extent(dk) / kKUnit); }
+
+int check_la(const Call& c, std::string* why) {
+  if (c.n_tiles != 4 || c.n_dims != 4 || c.n_dtypes != 3) {
+    *why = "expected 4 tiles, 4 dims (sq, sk, dk, dv) and 3 dtypes";
+    return AXON_EARG;
+  }
+  int rc = check_all_bf16(c, 3, why);
+  if (rc != AXON_OK) return rc;
+  const int64_t sq = c.dim(0), sk = c.dim(1), dk = c.dim(2), dv = c.dim(3);
+  rc = check_gemm_shape(dk, dv, sk, c.tile(3), c.tile(1), c.tile(2), why);
+  if (rc != AXON_OK) return rc;
+  return check_gemm_shape(sq, dv, dk, c.tile(0), c.tile(1), la_tk2(dk), why);
+}
+
+int manifest_la(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
+  if (cap < 4) return 0;
+  const int64_t state[3] = {dims[2], dims[3], dims[1]};  // dk x dv over sk
+  manifest_mm(v, state, dt, out, cap);
+  const int64_t sq = dims[0] > 0 ? dims[0] : 1;
+  out[3] = {"TILES_IN_BLOCK_P", out[0].extent, 64, false};
+  out[0] = {"TILES_IN_BLOCK_M", sq < 256 ? (sq < 64 ? 64 : sq) : 256, 64, false};
+  return 4;
+}
+
+struct LaLayout {
+  Plan p1, p2;
+  size_t kt, state, data, total;
+};
+
+// linear_attention workspace: [keyᵀ bf16 dk x sk][state bf16 dk x dv][split-K
+// data of whichever GEMM needs more].
+LaLayout la_layout(const Call& c) {
+  const int sq = static_cast<int>(c.dim(0)), sk = static_cast<int>(c.dim(1));
+  const int dk = static_cast<int>(c.dim(2)), dv = static_cast<int>(c.dim(3));
+  LaLayout L;
+  L.p1 = plan_of(dk, dv, sk, c.tile(3), c.tile(1), c.tile(2));
+  L.p2 = plan_of(sq, dv, dk, c.tile(0), c.tile(1), la_tk2(dk));
+  L.kt = 0;
+  L.state = align256(static_cast<size_t>(dk) * sk * sizeof(bf16));
+  L.data = L.state + align256(static_cast<size_t>(dk) * dv * sizeof(bf16));
+  const size_t d1 = data_bytes(L.p1, dk, dv, 1), d2 = data_bytes(L.p2, sq, dv, 1);
+  L.total = L.data + (d1 > d2 ? d1 : d2);
+  return L;
+}
+
+size_t workspace_la(const Call& c) { return la_layout(c).total; }
+
+void outputs_la(const int64_t* dims, const int32_t*, OutDesc* out) {
+  out[0] = {2, {dims[0], dims[3]}, AXON_BF16};
+}
+
+int launch_la(const Call& c, const void* const* in, void* const* out, void* ws, hipStream_t st) {
+  const int sq = static_cast<int>(c.dim(0)), sk = static_cast<int>(c.dim(1));
+  const int dk = static_cast<int>(c.dim(2)), dv = static_cast<int>(c.dim(3));
+  if (sq == 0 || dv == 0) return AXON_OK;
+  for (int i = 0; i < 3; ++i)
+    if (!aligned16(in[i])) {
+      set_error("linear_attention buffers must be 16-byte aligned");
+      return AXON_EARG;
+    }
+  const LaLayout L = la_layout(c);
+  if (!aligned16(out[0]) || ws == nullptr) {
+    set_error("linear_attention needs an aligned output and its workspace");
+    return AXON_EARG;
+  }
+  char* base = static_cast<char*>(ws);
+  bf16* kt = reinterpret_cast<bf16*>(base + L.kt);
+  bf16* state = reinterpret_cast<bf16*>(base + L.state);
+  int rc = launch_transpose(static_cast<const bf16*>(in[1]), kt, sk, dk, st);
+  if (rc != AXON_OK) return rc;
+  const GemmArgs g1 = make_args(kt, static_cast<const bf16*>(in[2]), nullptr, state, dk, dv, sk, L.p1,
+                                base + L.data, 1, 0.f);
+  rc = dispatch<kPlain, false>(L.p1.BM, L.p1.BN, g1, st, c.variant);
+  if (rc != AXON_OK) return rc;
+  const GemmArgs g2 = make_args(in[0], state, nullptr, out[0], sq, dv, dk, L.p2, base + L.data, 1, 0.f);
+  return dispatch<kPlain, false>(L.p2.BM, L.p2.BN, g2, st, c.variant);
+}
+
+const char* summary_la(int variant) {
+  return variant == 1
+             ? "keyᵀ into the workspace (LDS-tiled transpose), state = keyᵀ v as a split-K bf16 MFMA "
+               "GEMM (bf16 state), out = q state; both GEMMs on the hw variant 1 schedule"
+             : "keyᵀ into the workspace (LDS-tiled transpose), state = keyᵀ v as a split-K bf16 MFMA "
+               "GEMM (bf16 state), out = q state; both GEMMs on the hw variant 0 schedule";
+}
+
+// ---- attention (dims m, n, k; x [m,k], w_q, w_k, w_v [k,n]) ----------------
+// kernels/attention/kernel.py:7-18: q, k, v = x w_q, x w_k, x w_v (bf16 out,
+// fp32 accumulation); kᵀ into the workspace; S = q kᵀ in fp32 (m x m); out =
+// softmax(S) v with a bare exp/sum softmax: the kSoftmax GEMM on the fp32 S
+// (exp taken in fp32 as S is staged, split into bf16 hi + lo planes so the
+// probabilities keep fp32 accuracy), rows scaled by 1 / sum exp.
+// Tiles: TILES_IN_BLOCK_M = rows per tile / 64 (all stages),
+// TILES_IN_BLOCK_N = columns / 64 of the projections and of the output,
+// TILES_IN_BLOCK_P = columns / 64 of S, TILES_IN_BLOCK_K = K range / 256 of
+// every stage. The output stage holds two A planes, so its tile is narrowed
+// to BM <= 128 and BM x BN <= 128 x 128.
+struct AttnPlan {
+  Plan proj, s, pv;
+};
+
+AttnPlan attn_plan(const Call& c) {
+  const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1)), k = static_cast<int>(c.dim(2));
+  const int tm = c.tile(0), tn = c.tile(1), tk = c.tile(2), tp = c.tile(3);
+  const int tm2 = std::min(tm, 2), tn2 = std::max(1, std::min(tn, 4 / tm2));
+  AttnPlan P;
+  P.proj = plan_of(m, n, k, tm, tn, tk);
+  P.s = plan_of(m, m, n, tm, tp, tk);
+  P.pv = plan_of(m, n, m, tm2, tn2, tk);
+  return P;
+}
+
+int check_attn_qkv(const Call& c, std::string* why) {
+  if (c.n_tiles != 4 || c.n_dims != 3 || c.n_dtypes != 4) {
+    *why = "expected 4 tiles, 3 dims (m, n, k) and 4 dtypes";
+    return AXON_EARG;
+  }
+  int rc = check_all_bf16(c, 4, why);
+  if (rc != AXON_OK) return rc;
+  const int64_t m = c.dim(0), n = c.dim(1), k = c.dim(2);
+  if (m % 8 != 0) {
+    *why = "m must be a multiple of 8 (it is the column count of S)";
+    return AXON_EINVAL;
+  }
+  const int tm = c.tile(0), tn = c.tile(1), tk = c.tile(2), tp = c.tile(3);
+  rc = check_gemm_shape(m, n, k, tm, tn, tk, why);
+  if (rc == AXON_OK) rc = check_gemm_shape(m, m, n, tm, tp, tk, why);
+  if (rc == AXON_OK) rc = check_gemm_shape(m, n, m, tm, tn, tk, why);
+  return rc;
+}
+
+int manifest_attn_qkv(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
+  if (cap < 4) return 0;
+  const int64_t m = dims[0] > 0 ? dims[0] : 1;
+  // One K range serves all three contractions (over k, n and m).
+  const int64_t mnk[3] = {dims[0], dims[1], std::min({dims[0], dims[1], dims[2]})};
+  manifest_mm(v, mnk, dt, out, cap);
+  out[3] = {"TILES_IN_BLOCK_P", m < 256 ? (m < 64 ? 64 : m) : 256, 64, false};
+  return 4;
+}
+
+struct AttnLayout {
+  AttnPlan P;
+  size_t q, k, v, kt, s, data, total;
+};
+
+// attention workspace: [q][k][v] bf16 m x n each, [kᵀ] bf16 n x m, [S] fp32
+// m x m, [split-K data of the stage that needs most] (stages run in order
+// and share it).
+AttnLayout attn_layout(const Call& c) {
+  const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1));
+  AttnLayout L;
+  L.P = attn_plan(c);
+  const size_t mn = align256(static_cast<size_t>(m) * n * sizeof(bf16));
+  L.q = 0;
+  L.k = mn;
+  L.v = 2 * mn;
+  L.kt = 3 * mn;
+  L.s = 4 * mn;
+  L.data = L.s + align256(static_cast<size_t>(m) * m * sizeof(float));
+  const size_t d = std::max({data_bytes(L.P.proj, m, n, 1), data_bytes(L.P.s, m, m, 1), data_bytes(L.P.pv, m, n, 1)});
+  L.total = L.data + d;
+  return L;
+}
+
+size_t workspace_attn_qkv(const Call& c) { return attn_layout(c).total; }
+
+void outputs_attn_qkv(const int64_t* dims, const int32_t*, OutDesc* out) {
+  out[0] = {2, {dims[0], dims[1]}, AXON_BF16};
+}
+
+int launch_attn_qkv(const Call& c, const void* const* in, void* const* out, void* ws, hipStream_t st) {
+  const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1)), k = static_cast<int>(c.dim(2));
+  if (m == 0 || n == 0) return AXON_OK;
+  for (int i = 0; i < 4; ++i)
+    if (!aligned16(in[i])) {
+      set_error("attention buffers must be 16-byte aligned");
+      return AXON_EARG;
+    }
+  if (!aligned16(out[0]) || ws == nullptr) {
+    set_error("attention needs an aligned output and its workspace");
+    return AXON_EARG;
+  }
+  const AttnLayout L = attn_layout(c);
+  char* base = static_cast<char*>(ws);
+  bf16* q = reinterpret_cast<bf16*>(base + L.q);
+  bf16* kk = reinterpret_cast<bf16*>(base + L.k);
+  bf16* v = reinterpret_cast<bf16*>(base + L.v);
+  bf16* kt = reinterpret_cast<bf16*>(base + L.kt);
+  float* S = reinterpret_cast<float*>(base + L.s);
+  void* data = base + L.data;
+  bf16* proj_out[3] = {q, kk, v};
+  int rc = AXON_OK;
+  for (int i = 0; i < 3 && rc == AXON_OK; ++i) {
+    const GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[1 + i]), nullptr, proj_out[i], m, n, k,
+                                 L.P.proj, data, 1, 0.f);
+    rc = dispatch<kPlain, false>(L.P.proj.BM, L.P.proj.BN, g, st, c.variant);
+  }
+  if (rc == AXON_OK) rc = launch_transpose(kk, kt, m, n, st);
+  if (rc != AXON_OK) return rc;
+  GemmArgs gs = make_args(q, kt, nullptr, S, m, m, n, L.P.s, data, 1, 0.f);
+  gs.c_f32 = 1;
+  rc = dispatch<kPlain, false>(L.P.s.BM, L.P.s.BN, gs, st, c.variant);
+  if (rc != AXON_OK) return rc;
+  const GemmArgs gp = make_args(S, v, nullptr, out[0], m, n, m, L.P.pv, data, 1, 0.f);
+  return dispatch_mlp<kSoftmax, true>(L.P.pv.BM, L.P.pv.BN, gp, st);
+}
+
+const char* summary_attn_qkv(int variant) {
+  return variant == 1
+             ? "q, k, v projections and S = q kᵀ (fp32) as bf16 MFMA GEMMs on the hw variant 1 schedule, "
+               "kᵀ by an LDS-tiled transpose, then one GEMM over fp32 S with exp on staging (hi + lo "
+               "bf16 planes), row sums on the fly and 1/sum in the epilogue"
+             : "q, k, v projections and S = q kᵀ (fp32) as bf16 MFMA GEMMs on the hw variant 0 schedule, "
+               "kᵀ by an LDS-tiled transpose, then one GEMM over fp32 S with exp on staging (hi + lo "
+               "bf16 planes), row sums on the fly and 1/sum in the epilogue";
+}
+
 }  // namespace
 
 #define AXON_MM_FAMILY(fn_name, spec_name, EPI)                                                \
@@ -1236,6 +1539,24 @@ const Family* family_silu_mlp() {
 const Family* family_qkv_cte() {
   static const Family f = {"qkv_cte", 3, 4, 1, 3, kTileArgs3, 3, summary_qkv, manifest_qkv,
                            check_qkv, workspace_qkv, outputs_qkv, launch_qkv};
+  return &f;
+}
+
+const Family* family_softmax_mm() {
+  static const Family f = {"softmax_mm", 2, 2, 1, 3, kTileArgs3, 3, summary_softmax_mm, manifest_mm,
+                           check_mm<kSoftmax>, workspace_mm<kSoftmax>, outputs_mm, launch_mm<kSoftmax>};
+  return &f;
+}
+
+const Family* family_linear_attention() {
+  static const Family f = {"linear_attention", 2, 3, 1, 4, kTileArgs4, 4, summary_la, manifest_la,
+                           check_la, workspace_la, outputs_la, launch_la};
+  return &f;
+}
+
+const Family* family_attention_qkv() {
+  static const Family f = {"attention", 2, 4, 1, 3, kTileArgs4, 4, summary_attn_qkv, manifest_attn_qkv,
+                           check_attn_qkv, workspace_attn_qkv, outputs_attn_qkv, launch_attn_qkv};
   return &f;
 }
 

@@ -27,6 +27,9 @@ __all__ = [
     "rmsnorm_matmul_eps",
     "silu_mlp",
     "qkv_cte",
+    "softmax_mm",
+    "linear_attention",
+    "attention_qkv",
     "attention_nomax",
     "attention_causal",
     "ORACLE",
@@ -170,6 +173,29 @@ def qkv_cte(x, mlp_prev, attention_prev, w, eps=NORM_EPS):
     return (h * torch.rsqrt((h * h).mean(dim=-1, keepdim=True) + eps)) @ w
 
 
+def softmax_mm(x, w):
+    """(exp(x) / sum_k exp(x)) @ w, bare exp / sum (no max subtraction);
+    kernels/softmax_mm/refs.py:16-19, kernels/softmax_mm/kernel.py:7-11."""
+    x, w = _f32(x, w)
+    e = torch.exp(x)
+    return (e / e.sum(dim=-1, keepdim=True)) @ w
+
+
+def linear_attention(q, key, v):
+    """q @ (key^T @ v); kernels/linear_attention/refs.py:20-27."""
+    q, key, v = _f32(q, key, v)
+    return q @ (key.t() @ v)
+
+
+def attention_qkv(x, w_q, w_k, w_v):
+    """q, k, v = x w_q, x w_k, x w_v; softmax(q k^T) v with a bare exp / sum
+    softmax and no scale; kernels/attention/refs.py:16-36, kernel.py:7-18."""
+    x, w_q, w_k, w_v = _f32(x, w_q, w_k, w_v)
+    q, k, v = x @ w_q, x @ w_k, x @ w_v
+    e = torch.exp(q @ k.t())
+    return (e / e.sum(dim=-1, keepdim=True)) @ v
+
+
 def attention_nomax(q, k_t, v):
     """softmax(q @ k_t) @ v with a bare exp/sum softmax;
     kernels/attention_nkilib/refs.py:36-47."""
@@ -214,6 +240,9 @@ ORACLE = {
     "rmsnorm_matmul_eps": rmsnorm_matmul_eps,
     "silu_mlp": silu_mlp,
     "qkv_cte": qkv_cte,
+    "softmax_mm": softmax_mm,
+    "linear_attention": linear_attention,
+    "attention": attention_qkv,
     "attention_nkilib": attention_nomax,
     "attention_causal": attention_causal,
 }

@@ -66,7 +66,8 @@ def test_outputs_match_baseline_shapes(name):
     small = {"rope_llama3": (1, 8, 2, 1, 128), "attention_causal": (1, 2, 16, 128),
              "attention_nkilib": (16, 128), "silu_mlp": (16, 16, 16, 8), "fused_adam": (4, 16),
              "rope": (4, 16), "matmul": (8, 16, 16), "matmul_std002": (8, 16, 16),
-             "rmsnorm_matmul": (8, 16, 16), "rmsnorm_matmul_eps": (8, 16, 16), "qkv_cte": (8, 16, 16)}
+             "rmsnorm_matmul": (8, 16, 16), "rmsnorm_matmul_eps": (8, 16, 16), "qkv_cte": (8, 16, 16),
+             "softmax_mm": (8, 16, 16), "linear_attention": (8, 16, 16, 16), "attention": (16, 16, 16)}
     spec, dims, host = spec_inputs(name, small.get(name, (4, 64)))
     codes = [hip.AXON_BF16 if str(getattr(a, "dtype", "")).endswith("bfloat16") else hip.AXON_F32
              for a in host]

@@ -181,6 +181,39 @@ def pin_qkv_cte(fn):
     assert torch.allclose(fn(*big, w), fn(*[t * 2e3 for t in (x, mp, ap)], w), rtol=1e-4, atol=1e-5)
 
 
+def pin_softmax_mm(fn):
+    x, w = randn(9, 40), randn(40, 7)
+    ref = torch.softmax(x.double(), dim=-1) @ w.double()
+    assert torch.allclose(fn(x, w).double(), ref, rtol=1e-5, atol=1e-6)
+    # Each output row is a convex combination of the rows of w.
+    out = fn(x, torch.eye(40))
+    assert torch.allclose(out.sum(-1), torch.ones(9), atol=1e-5) and bool((out > 0).all())
+
+
+def pin_linear_attention(fn):
+    sq, sk, dk, dv = 12, 20, 8, 6
+    q, key, v = torch.rand(sq, dk), torch.rand(sk, dk), torch.rand(sk, dv)
+    # Evaluated the other way round, (q key^T) v, by the float64 C product.
+    scores = clib.matmul_f64(q.numpy(), key.t().contiguous().numpy())
+    ref = scores @ v.double().numpy()
+    assert np.allclose(fn(q, key, v).numpy(), ref, rtol=1e-5, atol=1e-5)
+    # Brute force on a tiny case: out[i][c] = sum_j (q_i . key_j) v[j][c].
+    bf = [[sum(float(q[i] @ key[j]) * float(v[j][c]) for j in range(sk)) for c in range(dv)] for i in range(2)]
+    assert np.allclose(fn(q, key, v)[:2].numpy(), np.array(bf), rtol=1e-5, atol=1e-5)
+
+
+def pin_attention_qkv(fn):
+    m, n, k = 24, 16, 32
+    x = randn(m, k)
+    w_q, w_k, w_v = randn(k, n, scale=0.1), randn(k, n, scale=0.1), randn(k, n, scale=0.2)
+    xd = x.double()
+    q, kk, v = xd @ w_q.double(), xd @ w_k.double(), xd @ w_v.double()
+    ref = F.scaled_dot_product_attention(q[None], kk[None], v[None], scale=1.0)[0]
+    assert torch.allclose(fn(x, w_q, w_k, w_v).double(), ref, rtol=1e-5, atol=1e-6)
+    c = clib.attention_head_f64(q.float().numpy(), kk.float().numpy(), v.float().numpy(), 1.0, False)
+    assert np.allclose(fn(x, w_q, w_k, w_v).numpy(), c, rtol=1e-4, atol=1e-5)
+
+
 # ---- attention ------------------------------------------------------------
 def pin_attention_nomax(fn):
     s, d = 40, 16
@@ -216,6 +249,9 @@ PINS = {
     "rmsnorm_matmul_eps": pin_rmsnorm_matmul_eps,
     "silu_mlp": pin_silu_mlp,
     "qkv_cte": pin_qkv_cte,
+    "softmax_mm": pin_softmax_mm,
+    "linear_attention": pin_linear_attention,
+    "attention_qkv": pin_attention_qkv,
     "attention_nomax": pin_attention_nomax,
     "attention_causal": pin_attention_causal,
 }
@@ -264,6 +300,19 @@ def _mutants():
     def qkv_no_eps(x, mp, ap, w):
         return oracle.qkv_cte(x, mp, ap, w, eps=0.0)
 
+    def softmax_mm_columns(x, w):
+        e = torch.exp(x)
+        return (e / e.sum(dim=0, keepdim=True)) @ w
+
+    def linear_attention_scaled(q, key, v):
+        return oracle.linear_attention(q, key, v) / key.shape[0]
+
+    def attention_qkv_scaled(x, w_q, w_k, w_v):
+        return oracle.attention_qkv(x, w_q / math.sqrt(w_q.shape[1]), w_k, w_v)
+
+    def attention_qkv_swapped(x, w_q, w_k, w_v):
+        return oracle.attention_qkv(x, w_k, w_q, w_v)
+
     def attn_no_mask(q, k, v):
         return F.scaled_dot_product_attention(q, k, v)
 
@@ -281,6 +330,10 @@ def _mutants():
         ("matmul", matmul_transposed),
         ("qkv_cte", qkv_two_residuals),
         ("qkv_cte", qkv_no_eps),
+        ("softmax_mm", softmax_mm_columns),
+        ("linear_attention", linear_attention_scaled),
+        ("attention_qkv", attention_qkv_scaled),
+        ("attention_qkv", attention_qkv_swapped),
         ("attention_causal", attn_no_mask),
         ("attention_causal", attn_no_scale),
     ]

@@ -18,7 +18,8 @@ SMALL = {
     "rope": (4, 16), "rope_llama3": (1, 8, 4, 2, 16), "cumsum": (4, 50), "cumsum_probs": (4, 50),
     "fused_adam": (4, 16), "matmul": (8, 4, 16), "matmul_std002": (8, 4, 16),
     "rmsnorm_matmul": (8, 4, 16), "rmsnorm_matmul_eps": (8, 4, 16), "silu_mlp": (8, 4, 16, 6),
-    "qkv_cte": (8, 4, 16), "attention_nkilib": (16, 8), "attention_causal": (1, 2, 16, 8),
+    "qkv_cte": (8, 4, 16), "softmax_mm": (8, 4, 16), "linear_attention": (8, 12, 4, 6),
+    "attention": (8, 4, 16), "attention_nkilib": (16, 8), "attention_causal": (1, 2, 16, 8),
 }
 
 
