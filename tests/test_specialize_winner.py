@@ -119,3 +119,25 @@ def test_device_id_from_rocminfo(monkeypatch):
     monkeypatch.setattr(sw.subprocess, "run", lambda *a, **k: R())
     d = sw.device_id()
     assert d.startswith("AMD GPU, gfx950, 256 CUs, 1 GPU agent(s)") and "Vendor" not in d
+
+
+@pytest.mark.parametrize("path", sorted((sw.REPO / "winners").glob("*.py")), ids=lambda p: p.stem)
+def test_committed_winners_are_legal_instantiations(path):
+    """Every tracked winner binds a tile tuple the library still accepts for
+    its kernel, hw variant and dims, and records a measurement."""
+    import ast
+
+    tree = ast.parse(path.read_text())
+    meta = next(ast.literal_eval(n.value) for n in tree.body
+                if isinstance(n, ast.Assign) and getattr(n.targets[0], "id", "") == "__axon_hip_kernel__")
+    fn = next(n for n in tree.body if isinstance(n, ast.FunctionDef))
+    tiles = {s.targets[0].id: s.value.value for s in fn.body
+             if isinstance(s, ast.Assign) and isinstance(s.value, ast.Constant)}
+    values = [tiles[t] for t in meta["tile_args"]]
+    dtype = hip.AXON_F32 if meta["kernel"] == "cumsum_probs" else hip.AXON_BF16
+    codes = [dtype] * len(meta["input_names"])
+    if meta["kernel"] == "rope_llama3":
+        codes = [hip.AXON_BF16, hip.AXON_BF16, hip.AXON_F32, hip.AXON_F32]
+    st, why = hip.check(meta["kernel"], meta["hw_variant"], values, meta["dims"], codes)
+    assert st == hip.AXON_OK, why
+    assert sw.recorded_us(path) is not None
