@@ -633,6 +633,255 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) 
 }
 
 // ---------------------------------------------------------------------------
+// hw variant 2 of the plain GEMM: direct-to-LDS loads (global_load_lds_dwordx4:
+// lane i's 16 bytes land at the wave's LDS base + 16 i), so tiles go from
+// memory to LDS without passing through registers, and NS LDS stages ring
+// with NS - 1 K steps of loads in flight. A wave's wait for its own loads
+// (vmcnt) plus the workgroup barrier make a stage visible to every wave; the
+// barrier also retires the reads of the stage the next loads overwrite.
+// Stage layout (16-byte chunks swizzled so fragment reads spread over banks):
+//   A: BM rows x 128 B; chunk kc of row r at slot kc ^ (r & 7);
+//   B: 64 k rows x BN columns as loaded; chunk c of row k at slot c ^ bg(k)
+//      with bg(k) = 2 ((k & 3) | ((k & 8) >> 1)) (2 (k & 3) for BN = 64), so
+//      the 8 rows one transposing read touches use distinct chunk slots.
+// Every K step is whole (k % 64 == 0). Rows of A past M and columns of B
+// past N are clamped reads that only feed discarded outputs. Steps past the
+// workgroup's K range reload its last step into the free stage (never read),
+// so the wait count is the same constant every step.
+// ---------------------------------------------------------------------------
+template <int BN>
+__device__ __forceinline__ int dma_bg(int k) {
+  if constexpr (BN >= 128) return 2 * ((k & 3) | ((k & 8) >> 1));
+  else return 2 * (k & 3);
+}
+
+__device__ __forceinline__ void dma16(const void* gptr, void* lds) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(gptr),
+                                   (__attribute__((address_space(3))) void*)(lds), 16, 0, 0);
+}
+
+// LDS fragment reads of hw variant 2, as inline assembly: the compiler
+// treats its own LDS reads after a global_load_lds as possibly aliasing the
+// loads in flight and waits for all of them (vmcnt(0)), which would drain
+// the stage ring every step. These reads are ordered by the explicit
+// vmcnt wait + barrier instead, and their results by lds_wait<N>().
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return static_cast<unsigned>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
+}
+
+__device__ __forceinline__ bf16x8 lds_read_b128(const void* p) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+__device__ __forceinline__ i16x4 lds_read_tr(const void* p) {
+  i16x4 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+  return r;
+}
+
+// Waits until at most N LDS operations are outstanding.
+template <int N>
+__device__ __forceinline__ void lds_wait() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
+}
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and
+// [15:14], expcnt[6:4] = 7, lgkmcnt[11:8] = 15).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM, int BN, int NS>
+constexpr size_t dma_lds_bytes() { return static_cast<size_t>(NS) * 128 * (BM + BN); }
+
+template <int BM, int BN, int EPI, int NS>
+__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(GemmArgs g) {
+  static_assert(EPI == kPlain, "hw variant 2 serves the plain epilogue");
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int SA = BM * 128, STAGE = (BM + BN) * 128;  // bytes
+  constexpr int LA = BM / 32, LB = BN / 32;  // DMA instructions per thread per K step
+  constexpr int CPR = BN / 8;                // 16-byte chunks per B row
+  constexpr int RPI = 64 / CPR;              // B rows per 1 KiB wave instruction
+  static_assert(NS >= 2 && TM >= 1 && TN >= 1, "tile shape");
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int G = g.S * g.MT * g.NT;
+  int unit = blockIdx.x;
+  if (G % kXcds == 0) unit = (blockIdx.x % kXcds) * (G / kXcds) + blockIdx.x / kXcds;
+  const int z = unit / (g.MT * g.NT);
+  const int tile = unit - z * g.MT * g.NT;
+  const int mt = tile / g.NT, nt = tile - mt * g.NT;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int kbeg = z * g.kchunk;
+  const int kend = min(g.K, kbeg + g.kchunk);
+  const int nsteps = (kend - kbeg) / BK;
+  const int klast = kbeg + max(nsteps - 1, 0) * BK;
+
+  const bf16* A = static_cast<const bf16*>(g.A);
+  // Per-lane source offsets (elements, without the step's k0).
+  int64_t a_off[LA];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) {
+    const int r = (i * 4 + wave) * 8 + (lane >> 3);
+    const int kc = (lane & 7) ^ (r & 7);
+    a_off[i] = static_cast<int64_t>(min(m0 + r, g.M - 1)) * g.K + kc * 8;
+  }
+  int b_row[LB], b_col[LB];
+#pragma unroll
+  for (int i = 0; i < LB; ++i) {
+    const int k = (i * 4 + wave) * RPI + lane / CPR;
+    const int c = (lane % CPR) ^ dma_bg<BN>(k);
+    b_row[i] = k;
+    b_col[i] = min(n0 + c * 8, g.N - 8);
+  }
+
+  auto issue = [&](int step, int stage) {
+    const int k0 = min(kbeg + step * BK, klast);
+    unsigned char* st = smem + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < LA; ++i) dma16(A + a_off[i] + k0, st + (i * 4 + wave) * 1024);
+#pragma unroll
+    for (int i = 0; i < LB; ++i)
+      dma16(g.B + static_cast<int64_t>(k0 + b_row[i]) * g.N + b_col[i], st + SA + (i * 4 + wave) * 1024);
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Fragment reads of one 16-deep slice kk of a stage into register set buf.
+  const int g4 = lane >> 4, s16 = lane & 15;
+  bf16x8 af[2][TM];
+  i16x4 bl[2][TN], bh[2][TN];
+  auto read = [&](int stage, int kk, int buf) {
+    const unsigned char* sa = smem + stage * STAGE;
+    const unsigned char* sb = sa + SA;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm * WM + i * 32 + (lane & 31);
+      const int kc = 2 * kk + (lane >> 5);
+      af[buf][i] = lds_read_b128(sa + r * 128 + ((kc ^ (r & 7)) << 4));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = wn * WN + j * 32 + 16 * (g4 & 1) + 4 * (s16 & 3);
+      const int c = n >> 3, half = (n >> 2) & 1;
+      const int k_lo = kk * 16 + 8 * (g4 >> 1) + (s16 >> 2), k_hi = k_lo + 4;
+      bl[buf][j] = lds_read_tr(sb + k_lo * (BN * 2) + ((c ^ dma_bg<BN>(k_lo)) << 4) + half * 8);
+      bh[buf][j] = lds_read_tr(sb + k_hi * (BN * 2) + ((c ^ dma_bg<BN>(k_hi)) << 4) + half * 8);
+    }
+  };
+  auto mfma = [&](int buf) {
+    // The fragments are opaque until here, so no MFMA moves above the wait.
+#pragma unroll
+    for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[buf][i]));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      asm volatile("" : "+v"(bl[buf][j]), "+v"(bh[buf][j]));
+      const bf16x8 bfr = __builtin_bit_cast(bf16x8, __builtin_shufflevector(bl[buf][j], bh[buf][j], 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[buf][i], bfr, acc[i][j], 0, 0, 0);
+    }
+  };
+  constexpr int NR = TM + 2 * TN;  // LDS reads per slice
+  static_assert(NR < 16, "reads per slice");
+
+  // Pipeline: step s lives in stage s % NS. Slice kk + 1 is read while slice
+  // kk's MFMAs wait only for their own reads; at the last slice of a step the
+  // wave finishes its reads of the stage, waits for its loads of the next
+  // step, meets the other waves at the barrier, refills the finished stage
+  // with step s + NS and reads the next step's first slice, all before the
+  // last slice's MFMAs, so no LDS latency is exposed at the step boundary.
+  constexpr int L = LA + LB;
+  if (nsteps > 0) {
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue(s, s);
+    wait_vmcnt<(NS - 2) * L>();
+    __builtin_amdgcn_s_barrier();
+    issue(NS - 1, NS - 1);
+    read(0, 0, 0);
+    int stage = 0;
+    for (int t = 0; t < nsteps; ++t) {
+      const int next = stage == NS - 1 ? 0 : stage + 1;
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        const int cur = kk & 1;
+        if (kk + 1 < BK / 16) {
+          read(stage, kk + 1, cur ^ 1);
+          lds_wait<NR>();
+        } else if (t + 1 < nsteps) {
+          lds_wait<0>();
+          wait_vmcnt<(NS - 2) * L>();
+          __builtin_amdgcn_s_barrier();
+          issue(t + NS, stage);
+          read(next, 0, cur ^ 1);
+        } else {
+          lds_wait<0>();
+        }
+        mfma(cur);
+      }
+      stage = next;
+    }
+    // Drain the loads past the K range before the workgroup's LDS goes away.
+    wait_vmcnt<0>();
+  }
+
+  auto row_of = [&](int i, int e) { return wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); };
+  auto col_of = [&](int j) { return wn * WN + j * 32 + (lane & 31); };
+  if (g.S == 1) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int gm = m0 + row_of(i, e);
+        if (gm >= g.M) continue;
+        const float sc = g.rscale != nullptr ? g.rscale[gm] : 1.f;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int gn = n0 + col_of(j);
+          if (gn >= g.N) continue;
+          const int64_t o = static_cast<int64_t>(gm) * g.N + gn;
+          if (g.c_f32) static_cast<float*>(g.C)[o] = acc[i][j][e] * sc;
+          else static_cast<bf16*>(g.C)[o] = static_cast<bf16>(acc[i][j][e] * sc);
+        }
+      }
+    return;
+  }
+  const int64_t MN = static_cast<int64_t>(g.M) * g.N;
+  float* dst = g.partial + static_cast<int64_t>(z) * MN;
+  const bool whole = m0 + BM <= g.M && n0 + BN <= g.N;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int gm = m0 + row_of(i, e);
+      if (!whole && gm >= g.M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int gn = n0 + col_of(j);
+        if (!whole && gn >= g.N) continue;
+        dst[static_cast<int64_t>(gm) * g.N + gn] = acc[i][j][e];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // qkv_cte operand preparation (kernels/qkv_cte/kernel.py:22-27): one
 // workgroup per row streams the three residual inputs once, forms
 // h = (x + mlp_prev) + attention_prev in fp32 (the reference's order),
@@ -830,6 +1079,52 @@ void launch_tile(const GemmArgs& g, hipStream_t st) {
   }
 }
 
+// hw variant 2 (direct-to-LDS loads): as many LDS stages as fit, at most 4.
+constexpr int dma_ns(int BM, int BN) {
+  return static_cast<int>(kMaxLds / (128 * static_cast<size_t>(BM + BN))) < 4
+             ? static_cast<int>(kMaxLds / (128 * static_cast<size_t>(BM + BN)))
+             : 4;
+}
+
+template <int BM, int BN, int EPI>
+void launch_dma_tile(const GemmArgs& g, hipStream_t st) {
+  constexpr int NS = dma_ns(BM, BN);
+  constexpr size_t lds = dma_lds_bytes<BM, BN, NS>();
+  static_assert(lds <= kMaxLds, "LDS budget");
+  auto fn = gemm_dma_kernel<BM, BN, EPI, NS>;
+  static std::atomic<bool> configured{false};
+  if (!configured.load(std::memory_order_acquire)) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(lds));
+    configured.store(true, std::memory_order_release);
+  }
+  const unsigned blocks = static_cast<unsigned>(g.S * g.MT * g.NT);
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(kThreads), lds, st, g);
+  if (g.S > 1) {
+    const int64_t quads = static_cast<int64_t>(g.M) * g.N / 4;
+    hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3(static_cast<unsigned>((quads + 255) / 256)),
+                       dim3(256), 0, st, g, BN);
+  }
+}
+
+template <int EPI>
+int dispatch_dma(int BM, int BN, const GemmArgs& g, hipStream_t st) {
+#define AXON_GEMM_CASE(bm, bn) \
+  if (BM == bm && BN == bn) { launch_dma_tile<bm, bn, EPI>(g, st); return launch_status("gemm_dma_kernel"); }
+  AXON_GEMM_CASE(64, 64)
+  AXON_GEMM_CASE(64, 128)
+  AXON_GEMM_CASE(64, 256)
+  AXON_GEMM_CASE(128, 64)
+  AXON_GEMM_CASE(128, 128)
+  AXON_GEMM_CASE(128, 256)
+  AXON_GEMM_CASE(256, 64)
+  AXON_GEMM_CASE(256, 128)
+  AXON_GEMM_CASE(256, 256)
+#undef AXON_GEMM_CASE
+  set_error("no GEMM instantiation for this tile");
+  return AXON_EINVAL;
+}
+
 // Prefetch depth of hw variant 1 (register sets of loads in flight).
 constexpr int deep_pd(int BM, int BN) { return BM * BN <= 128 * 128 ? 3 : 2; }
 
@@ -956,6 +1251,27 @@ int manifest_mm(int, const int64_t* dims, int, Constraint* out, int cap) {
   return 3;
 }
 
+// The plain matmul families have a third hw variant (direct-to-LDS loads)
+// that needs whole 64-deep K steps.
+constexpr int kDmaVariant = 2;
+
+int check_plain(const Call& c, std::string* why) {
+  const int rc = check_mm<kPlain>(c, why);
+  if (rc != AXON_OK) return rc;
+  if (c.variant == kDmaVariant && c.dim(2) % BK != 0) {
+    *why = "hw variant 2 loads whole 64-deep K steps: k must be a multiple of 64";
+    return AXON_EINVAL;
+  }
+  return AXON_OK;
+}
+
+int manifest_plain(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
+  const int n = manifest_mm(v, dims, dt, out, cap);
+  if (v == kDmaVariant && dims[2] % BK != 0)
+    for (int i = 0; i < n; ++i) out[i].extent = 0;  // admits no tile
+  return n;
+}
+
 template <int EPI>
 size_t workspace_mm(const Call& c) {
   return gemm_workspace(static_cast<int>(c.dim(0)), static_cast<int>(c.dim(1)),
@@ -977,10 +1293,18 @@ int launch_mm(const Call& c, const void* const* in, void* const* out, void* ws, 
   const Plan p = plan_of(M, N, K, c.tile(0), c.tile(1), c.tile(2));
   const GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[1]), nullptr, out[0], M, N, K, p, ws,
                                1, 1e-6f);
+  if constexpr (EPI == kPlain) {
+    if (c.variant == kDmaVariant) return dispatch_dma<kPlain>(p.BM, p.BN, g, st);
+  }
   return dispatch<EPI, false>(p.BM, p.BN, g, st, c.variant);
 }
 
 const char* summary_mm(int variant) {
+  if (variant == kDmaVariant)
+    return "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, A and B tiles loaded straight into LDS "
+           "(global_load_lds_dwordx4, chunk-swizzled stages, up to 4 stages = 3 K steps in flight), "
+           "B fragments by the transposing LDS read, split-K with a parallel fixup kernel, XCD-grouped "
+           "K ranges; needs k % 64 == 0";
   return variant == 1
              ? "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, 2-3 K steps of global loads in flight in "
                "rotating register sets, LDS double buffer with B transposed on store, split-K with a "
@@ -1524,8 +1848,17 @@ const char* summary_attn_qkv(int variant) {
     return &f;                                                                               \
   }
 
-AXON_MM_FAMILY(family_matmul, "matmul", kPlain)
-AXON_MM_FAMILY(family_matmul_std002, "matmul_std002", kPlain)
+#define AXON_PLAIN_FAMILY(fn_name, spec_name)                                                    \
+  const Family* fn_name() {                                                                    \
+    static const Family f = {spec_name,     3,          2,              1,           3,        \
+                             kTileArgs3,    3,          summary_mm,     manifest_plain, check_plain, \
+                             workspace_mm<kPlain>, outputs_mm, launch_mm<kPlain>};               \
+    return &f;                                                                                 \
+  }
+
+AXON_PLAIN_FAMILY(family_matmul, "matmul")
+AXON_PLAIN_FAMILY(family_matmul_std002, "matmul_std002")
+#undef AXON_PLAIN_FAMILY
 AXON_MM_FAMILY(family_rmsnorm_matmul, "rmsnorm_matmul", kRmsSum)
 AXON_MM_FAMILY(family_rmsnorm_matmul_eps, "rmsnorm_matmul_eps", kRmsEps)
 #undef AXON_MM_FAMILY

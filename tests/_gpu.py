@@ -32,10 +32,15 @@ def check_parity(name, sizes, *, rtol, atol, variants=None, budget=0, dtype=None
     dvals = [dims[d] for d in spec.dim_vars]
     if want is None:
         want = as_tuple(oracle.ORACLE[name](*[t.cpu() for t in dev]))
+    explicit = variants is not None
     variants = range(hip.variant_count(name)) if variants is None else variants
     checked = 0
     for v in variants:
         tiles = legal_tiles(name, v, dvals, codes, len(spec.tile_args))
+        # A variant may not serve every shape (hw variant 2 of the plain GEMM
+        # needs k % 64 == 0); asked for explicitly, it must.
+        if not tiles and not explicit:
+            continue
         assert tiles, f"{name} v{v}: no legal tile tuple for {sizes}"
         if budget:
             tiles = select_diverse(tiles, budget=budget, seed=42)
@@ -53,4 +58,5 @@ def check_parity(name, sizes, *, rtol, atol, variants=None, budget=0, dtype=None
                     msg=lambda m, v=v, t=t, i=i: f"{name} v{v} tiles {t} out{i}: {m}",
                 )
             checked += 1
+    assert checked, f"{name}: no hw variant has a legal tile tuple for {sizes}"
     return checked
