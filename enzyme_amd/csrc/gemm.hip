@@ -1564,10 +1564,12 @@ const char* summary_qkv(int variant) {
 // (row pitch 66 elements: the column reads of one wave touch distinct banks).
 constexpr int kTp = 64;
 
+// Grid: x over row tiles (the long side here: sequence positions), y over
+// column tiles.
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const bf16* __restrict__ in,
                                                             bf16* __restrict__ out, int R, int C) {
   __shared__ bf16 tile[kTp][kTp + 2];
-  const int r0 = blockIdx.y * kTp, c0 = blockIdx.x * kTp;
+  const int r0 = blockIdx.x * kTp, c0 = blockIdx.y * kTp;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
 #pragma unroll
   for (int i = 0; i < kTp; i += 4) {
@@ -1584,7 +1586,11 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const bf16* __restr
 
 int launch_transpose(const bf16* in, bf16* out, int R, int C, hipStream_t st) {
   if (R == 0 || C == 0) return AXON_OK;
-  const dim3 grid((C + kTp - 1) / kTp, (R + kTp - 1) / kTp);
+  if ((C + kTp - 1) / kTp > 65535) {
+    set_error("transpose: more than 65535 column tiles");
+    return AXON_EINVAL;
+  }
+  const dim3 grid((R + kTp - 1) / kTp, (C + kTp - 1) / kTp);
   hipLaunchKernelGGL(transpose_bf16_kernel, grid, dim3(256), 0, st, in, out, R, C);
   return launch_status("transpose_bf16_kernel");
 }
@@ -1629,6 +1635,10 @@ int check_la(const Call& c, std::string* why) {
   int rc = check_all_bf16(c, 3, why);
   if (rc != AXON_OK) return rc;
   const int64_t sq = c.dim(0), sk = c.dim(1), dk = c.dim(2), dv = c.dim(3);
+  if (dk > 65535LL * kTp) {
+    *why = "dk out of range";
+    return AXON_EINVAL;
+  }
   rc = check_gemm_shape(dk, dv, sk, c.tile(3), c.tile(1), c.tile(2), why);
   if (rc != AXON_OK) return rc;
   return check_gemm_shape(sq, dv, dk, c.tile(0), c.tile(1), la_tk2(dk), why);
@@ -1742,6 +1752,10 @@ int check_attn_qkv(const Call& c, std::string* why) {
   const int64_t m = c.dim(0), n = c.dim(1), k = c.dim(2);
   if (m % 8 != 0) {
     *why = "m must be a multiple of 8 (it is the column count of S)";
+    return AXON_EINVAL;
+  }
+  if (n > 65535LL * kTp) {
+    *why = "n out of range";
     return AXON_EINVAL;
   }
   const int tm = c.tile(0), tn = c.tile(1), tk = c.tile(2), tp = c.tile(3);
