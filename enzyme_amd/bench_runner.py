@@ -778,6 +778,31 @@ def time_cpu_reference(fn, inputs, *, warmup: int = 3, runs: int = 10, threads: 
     return BenchStats.from_durations(times), torch.get_num_threads()
 
 
+def time_gpu_reference(fn, inputs, *, warmup: int = 3, runs: int = 10):
+    """Per-call HIP-event times (ms) of `fn` run eagerly by torch-ROCm on the
+    GPU, on fp32 copies of the inputs already resident in HBM (the torch_ref
+    wrapper's fp32 coercion, case_gen.py:190-201 of the reference), with
+    tensors a reference creates inside defaulting to the GPU. Returns the
+    stats and the device name."""
+    import torch
+
+    args = [_dt.to_f32_torch(a).cuda() for a in inputs]
+    times = []
+    with torch.no_grad(), torch.device("cuda"):
+        for _ in range(warmup):
+            fn(*args)
+        torch.cuda.synchronize()
+        for _ in range(runs):
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            fn(*args)
+            end.record()
+            end.synchronize()
+            times.append(start.elapsed_time(end))
+    return BenchStats.from_durations(times), torch.cuda.get_device_name(0)
+
+
 def run_baseline(
     spec: KernelSpec,
     dim_sizes: dict[str, int],
@@ -788,17 +813,23 @@ def run_baseline(
     target: str | None = None,
     dtype: Any | None = None,
 ) -> str:
-    """`--mode baseline`: the spec's `torch_ref` (or `baseline_op`) timed on
-    the host CPU cores, appended to the baseline CSV (the reference times a
-    numpy-on-device baseline here, src/axon/bench_runner.py:828-889)."""
+    """`--mode baseline`: the reference compiles the spec's numpy baseline
+    for the device and benches it there (src/axon/bench_runner.py:828-889);
+    here the spec's `torch_ref` runs eagerly on the GPU through torch-ROCm
+    (its vendor-library kernels: hipBLASLt, MIOpen, ...) on fp32 inputs
+    resident in HBM, timed per call with HIP events. Without a visible GPU it
+    is timed on the host CPU cores instead. One row is appended to the
+    baseline CSV with a `device` column saying which."""
     del target
     fn = spec.torch_ref
     if fn is None and spec.baseline_op is None:
         raise ValueError(f"kernel '{spec.name}' has no baseline_op set")
     import pandas as pd
+    import torch
 
+    on_gpu = torch.cuda.is_available()
     print("\n" + "=" * 80)
-    print(f"CPU TORCH BASELINE {spec.name.upper()}")
+    print(f"{'GPU TORCH-ROCM' if on_gpu else 'CPU TORCH'} BASELINE {spec.name.upper()}")
     print("=" * 80)
     ordered_dims, ordered_sizes = _ordered_sizes(spec, dim_sizes)
     paths.baseline_dir.mkdir(parents=True, exist_ok=True)
@@ -810,13 +841,18 @@ def run_baseline(
         base = spec.baseline_op
 
         def fn(*xs):
-            return base(*[x.numpy() for x in xs])
+            return base(*[x.cpu().numpy() for x in xs])
 
-    stats, threads = time_cpu_reference(fn, inputs, warmup=max(1, warmup), runs=max(1, bench))
+    if on_gpu and spec.torch_ref is not None:
+        stats, name = time_gpu_reference(fn, inputs, warmup=max(1, warmup), runs=max(1, bench))
+        extra = {"device": f"gpu: {name} (torch-ROCm eager, fp32 inputs)"}
+    else:
+        stats, threads = time_cpu_reference(fn, inputs, warmup=max(1, warmup), runs=max(1, bench))
+        extra = {"device": "cpu", "cpu_threads": threads}
     row = {
         **{k: v for k, v in asdict(stats).items() if k != "outputs"},
         **dict(zip(ordered_dims, ordered_sizes, strict=True)),
-        "cpu_threads": threads,
+        **extra,
     }
     df = pd.DataFrame([row])
     print(f"\nBaseline {spec.name} Results:")
