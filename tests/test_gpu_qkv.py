@@ -98,3 +98,28 @@ def test_qkv_repeated_launches_bit_identical(dtype, variant):
     assert torch.equal(first, ln.outputs[0])
     ref = oracle.qkv_cte(*[t.cpu() for t in dev])
     torch.testing.assert_close(first.float().cpu(), ref, rtol=2e-2, atol=2e-2)
+
+
+@pytest.mark.parametrize(("sizes", "dtype", "variant"),
+                         [((16384, 640, 12288), torch.bfloat16, 2), ((16384, 640, 12288), torch.bfloat16, 1),
+                          ((8192, 512, 16384), torch.float32, 1)],
+                         ids=["mistral123b-v2", "mistral123b-v1", "llama405b_8k_fp32-v1"])
+def test_qkv_large_reference_cases(sizes, dtype, variant):
+    """The reference's mistral123b (n = 640: a ragged last N tile at 128 or
+    256 columns) and llama405b_8k fp32 cases at full size, inputs drawn on
+    the GPU, against torch's fp32 restatement of the reference formula, at
+    the reference's tolerances (bf16: rtol 5e-2, atol 1.5e-1; fp32: 1e-3)."""
+    m, n, k = sizes
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x, mp, ap = (torch.randn(m, k, device="cuda", generator=g).to(dtype) for _ in range(3))
+    w = (torch.randn(k, n, device="cuda", generator=g) / np.sqrt(k)).to(dtype)
+    codes = [hip.dtype_code(x)] * 4
+    tiles = (2, 2, 8)
+    assert hip.check("qkv_cte", variant, tiles, [m, n, k], codes)[0] == hip.AXON_OK
+    ln = hip.Launcher("qkv_cte", variant, tiles, [m, n, k], [x, mp, ap, w])
+    ln.launch()
+    torch.cuda.synchronize()
+    h = (x.float() + mp.float()) + ap.float()
+    ref = (h * torch.rsqrt((h * h).mean(dim=-1, keepdim=True) + 1e-6)) @ w.float()
+    tol = (1e-3, 1e-3) if dtype == torch.float32 else (5e-2, 1.5e-1)
+    torch.testing.assert_close(ln.outputs[0].float(), ref, rtol=tol[0], atol=tol[1])
