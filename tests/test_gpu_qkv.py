@@ -102,13 +102,16 @@ def test_qkv_repeated_launches_bit_identical(dtype, variant):
 
 @pytest.mark.parametrize(("sizes", "dtype", "variant"),
                          [((16384, 640, 12288), torch.bfloat16, 2), ((16384, 640, 12288), torch.bfloat16, 1),
-                          ((8192, 512, 16384), torch.float32, 1)],
-                         ids=["mistral123b-v2", "mistral123b-v1", "llama405b_8k_fp32-v1"])
+                          ((8192, 512, 16384), torch.bfloat16, 2), ((8192, 512, 16384), torch.float32, 1),
+                          ((16384, 512, 8192), torch.float32, 0), ((16384, 640, 12288), torch.float32, 1)],
+                         ids=["mistral123b-v2", "mistral123b-v1", "llama405b_8k-v2", "llama405b_8k_fp32-v1",
+                              "llama70b_fp32-v0", "mistral123b_fp32-v1"])
 def test_qkv_large_reference_cases(sizes, dtype, variant):
-    """The reference's mistral123b (n = 640: a ragged last N tile at 128 or
-    256 columns) and llama405b_8k fp32 cases at full size, inputs drawn on
-    the GPU, against torch's fp32 restatement of the reference formula, at
-    the reference's tolerances (bf16: rtol 5e-2, atol 1.5e-1; fp32: 1e-3)."""
+    """The reference's large cases (mistral123b, n = 640: a ragged last N tile
+    at 128 or 256 columns; llama405b_8k; the fp32 llama70b / mistral123b /
+    llama405b_8k) at full size, inputs drawn on the GPU, against torch's fp32
+    restatement of the reference formula, at the reference's tolerances
+    (bf16: rtol 5e-2, atol 1.5e-1; fp32: 1e-3)."""
     m, n, k = sizes
     g = torch.Generator(device="cuda").manual_seed(5)
     x, mp, ap = (torch.randn(m, k, device="cuda", generator=g).to(dtype) for _ in range(3))
