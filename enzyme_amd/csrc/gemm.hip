@@ -53,6 +53,7 @@ namespace axon {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
@@ -265,14 +266,18 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         }
         store_vec(As + ((buf * NA + 0) * BM + r) * LDK + kc, t);
         if constexpr (EPI == kRmsSum || EPI == kRmsEps) {
+          // Sum of squares straight from the bf16 pairs: v_dot2c_f32_bf16
+          // (exact bf16 products, fp32 accumulation), 4 instructions for 8
+          // values instead of 8 conversions and 8 FMAs.
+          const bf16x2* pr = reinterpret_cast<const bf16x2*>(&t);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = to_f32(t.v[e]);
+          for (int q = 0; q < 4; ++q) sq[j] = __builtin_amdgcn_fdot2_f32_bf16(pr[q], pr[q], sq[j], false);
         }
       }
       if constexpr (EPI == kSoftmax) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) sq[j] += x[e];
-      } else if constexpr (is_rms<EPI>()) {
+      } else if constexpr (EPI == kQkv || (A_F32 && is_rms<EPI>())) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) sq[j] += x[e] * x[e];
       }
