@@ -14,13 +14,17 @@ over enough copies of the input/output set to exceed 1 GiB, so the 256 MB
 Infinity Cache cannot serve a set that was just touched. `--warmup` untimed
 launches, then exactly `--steps` launches between two HIP events recorded on
 the stream the kernels are launched on, bracketed by device syncs; the
-average launch duration is the elapsed time / steps.
+average launch duration is the elapsed time / steps. After an idle second
+(the CPU baseline legs leave the GPU idle) the clocks take about 30 ms of
+back-to-back launches to settle: the 33 us matmul runs its first launches
+at 240 us and its next 25 at 42 us, so the default warmup of 2000 launches
+keeps every workload's ramp out of the timed region.
 
 CPU baseline: the oracle restatement of the same math, timed on the host
 cores (torch, all affinity cores) on the full headline shape; its output is
 also compared with the GPU output as a last guard.
 
-Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--headline-only]
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 2000] [--headline-only]
 """
 
 from __future__ import annotations
@@ -210,7 +214,7 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args(argv)
@@ -278,7 +282,7 @@ def main(argv=None) -> int:
     if not args.headline_only:
         rows = []
         for cfg in CONFIGS:
-            steps = max(20, args.steps // (4 if cfg["bound"] == "mfma" else 1))
+            steps = args.steps
             us, o, h, _ = measure(cfg, steps, args.warmup)
             row = {"spec": cfg["spec"], "label": cfg["label"], "tiles": list(cfg["tiles"]),
                    "hw_variant": cfg["variant"], "us_per_launch": round(us, 3), **roofline(cfg, us),

@@ -28,7 +28,11 @@ What the workers do is this backend's own:
   copies the inputs to HBM, and times each launch with a pair of HIP events
   on the launch stream. To keep the 256 MB Infinity Cache from serving
   inputs, launches rotate over enough copies of the input/output set to
-  exceed `AXON_ROTATE_BYTES` (default 1 GiB).
+  exceed `AXON_ROTATE_BYTES` (default 1 GiB). After the requested warmup
+  launches it keeps launching until `AXON_SETTLE_MS` (default 50 ms) of
+  launches have run: after host-side gaps the clocks take ~30 ms of
+  back-to-back launches to settle, and a 30 us kernel timed straight after
+  20 warmups reads 10-20 % slow.
 """
 
 from __future__ import annotations
@@ -72,6 +76,8 @@ __all__ = [
 DEFAULT_TARGET = "gfx950"
 ROTATE_BYTES_DEFAULT = 1 << 30
 MAX_ROTATE_SETS = 64
+SETTLE_MS_DEFAULT = 50.0
+MAX_SETTLE_LAUNCHES = 100_000
 HIP_META_NAME = "__axon_hip_kernel__"
 
 
@@ -254,10 +260,28 @@ def _bench_one_artifact(args) -> BenchStats:
         sets.append(([t.clone() for t in set0], [torch.empty_like(o) for o in ln.outputs]))
 
     stream = torch.cuda.current_stream(dev)
-    for i in range(max(0, int(warmup))):
-        ln.rebind(*sets[i % n_sets])
+    settle_ms = float(os.environ.get("AXON_SETTLE_MS") or SETTLE_MS_DEFAULT)
+    w0 = torch.cuda.Event(enable_timing=True)
+    w1 = torch.cuda.Event(enable_timing=True)
+    w0.record(stream)
+    done = 0
+    for _ in range(max(0, int(warmup))):
+        ln.rebind(*sets[done % n_sets])
         ln.launch(stream)
+        done += 1
+    w1.record(stream)
     torch.cuda.synchronize(dev)
+    # Clock settle: extend the warmup in doubling chunks until the untimed
+    # launches have covered settle_ms of device time.
+    chunk = max(1, done)
+    while settle_ms > 0 and w0.elapsed_time(w1) < settle_ms and done < MAX_SETTLE_LAUNCHES:
+        for _ in range(chunk):
+            ln.rebind(*sets[done % n_sets])
+            ln.launch(stream)
+            done += 1
+        w1.record(stream)
+        torch.cuda.synchronize(dev)
+        chunk *= 2
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(bench)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(bench)]
     for i in range(bench):
