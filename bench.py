@@ -51,6 +51,10 @@ METRIC = "achieved HBM GB/s (% peak) per norm/rope/scan; MFMA TFLOP/s for matmul
 
 # name, sizes, variant, tiles (picked by the tile sweep on MI355X), bound,
 # algorithmic work per launch (bytes for "hbm", FLOPs for "mfma"), label.
+# The bound is the larger of the two lower limits, bytes / 8 TB/s and
+# FLOPs / 2.5 PFLOP/s: qkv_cte's three [16384,8192] residual inputs make it
+# HBM-bound (830 MB: 104 us) although it is a GEMM (137 GFLOP: 55 us); its
+# row also reports the MFMA rate (`flops`).
 CONFIGS = [
     dict(
         spec="rope_llama3", sizes=(1, 4096, 32, 8, 128), variant=0, tiles=(4, 1), bound="hbm",
@@ -83,8 +87,8 @@ CONFIGS = [
         label="causal attention Q/K/V [1,32,4096,128] bf16, scale 1/sqrt(128)",
     ),
     dict(
-        spec="qkv_cte", sizes=(16384, 512, 8192), variant=2, tiles=(4, 4, 16), bound="mfma",
-        work=2 * 16384 * 512 * 8192,
+        spec="qkv_cte", sizes=(16384, 512, 8192), variant=2, tiles=(4, 4, 16), bound="hbm",
+        work=3 * 16384 * 8192 * 2 + 8192 * 512 * 2 + 16384 * 512 * 2, flops=2 * 16384 * 512 * 8192,
         label="qkv_cte llama70b: x, mlp_prev, attention_prev [16384,8192] bf16 summed, RMSNorm eps 1e-6, "
               "@ w [8192,512] bf16",
     ),
@@ -287,6 +291,10 @@ def main(argv=None) -> int:
             row = {"spec": cfg["spec"], "label": cfg["label"], "tiles": list(cfg["tiles"]),
                    "hw_variant": cfg["variant"], "us_per_launch": round(us, 3), **roofline(cfg, us),
                    "traffic": traffic_for(cfg["spec"])}
+            if "flops" in cfg:
+                tf = cfg["flops"] / (us * 1e-6) / 1e12
+                row["mfma"] = {"achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                               "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
             if cfg["bound"] == "hbm":
                 cu = measure_copy(cfg["work"] // 2, steps, args.warmup)
                 row["copy_us"] = round(cu, 3)
