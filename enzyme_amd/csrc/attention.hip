@@ -360,7 +360,9 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
 // running while the same wave issues other instructions), then O += V(j)^T
 // P(j). At the end of iteration j the block's loads land: K(j+2) into the
 // buffer K(j) left (last read in iteration j-1) and V(j+1) into the buffer
-// V(j-1) left; one barrier per block. 4 or 8 waves of 32 queries.
+// V(j-1) left; one barrier per block. 4 or 8 waves of 32 queries. Causal:
+// a wave skips the compute of blocks past its last query (it still stages
+// K and V and meets the barrier with the others).
 template <int W, int TN, bool CAUSAL, bool KT>
 __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
   constexpr int NT = W * 64;
@@ -400,7 +402,11 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
   bf16* O = a.o + base;
 
   const int q0 = qb * BQ;
-  const int qw = q0 + wave * 32;
+  // Waves w and w + W/2 share a SIMD: pairing an early query tile with a
+  // late one gives every SIMD the same number of skipped (fully masked)
+  // blocks at the diagonal.
+  const int wq = wave < W / 2 ? wave : 3 * W / 2 - 1 - wave;
+  const int qw = q0 + wq * 32;
   const int my_q = qw + (lane & 31);
   const int kv_end = CAUSAL ? min(a.s, q0 + BQ) : a.s;
   const int nblocks = (kv_end + BKV - 1) / BKV;
@@ -583,8 +589,10 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
   auto iter = [&](int j, auto par_tag) {
     load_k((j + 2) * BKV);
     load_v((j + 1) * BKV);
-    if (qw < a.s) {
-      const int kv0 = j * BKV;
+    const int kv0 = j * BKV;
+    // A block past the wave's last query contributes nothing, and neither
+    // does any later one, whose scores S(j+1) the skipped body would compute.
+    if (qw < a.s && !(CAUSAL && kv0 > qw + 31)) {
       if ((CAUSAL && kv0 + BKV - 1 > qw) || kv0 + BKV > a.s) body(std::true_type{}, par_tag, j);
       else body(std::false_type{}, par_tag, j);
     }
