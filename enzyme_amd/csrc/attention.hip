@@ -561,7 +561,9 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
       m_run = m_new;
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    m1(acc_s[P ^ 1], j + 1);
+    // A masked block is the wave's last one (its diagonal, or the end of the
+    // sequence): no later block needs S(j+1).
+    if constexpr (!MASK) m1(acc_s[P ^ 1], j + 1);
     float lblk = 0.f;
 #pragma unroll
     for (int t = 0; t < TN; ++t)
