@@ -96,6 +96,13 @@ struct GemmArgs {
   int S, MT, NT;
   float eps;
   int c_f32;            // kPlain: C is fp32 instead of bf16
+  // Column-split operands (kPlain, hw variants 0/1): with ncol > 0 the
+  // logical B [K, N] is [B | Bcol[0] | Bcol[1]] and C [M, N] is
+  // [C | Ccol[0] | Ccol[1]], each block ncol columns wide and contiguous on
+  // its own (N = 3 ncol, ncol a multiple of BN, so a tile never straddles).
+  const bf16* Bcol[2];
+  void* Ccol[2];
+  int ncol;
 };
 
 __device__ __forceinline__ float silu(float a) { return a / (1.f + __expf(-a)); }
@@ -139,6 +146,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   const int m0 = mt * BM, n0 = nt * BN;
   const int kbeg = z * g.kchunk;
   const int kend = min(g.K, kbeg + g.kchunk);
+  // This tile's B and C blocks (the whole of B and C unless column-split).
+  const int csel = g.ncol > 0 ? n0 / g.ncol : 0;
+  const int ncol0 = csel * g.ncol;
+  const int ldbc = g.ncol > 0 ? g.ncol : g.N;
+  const bf16* Bw = csel == 0 ? g.B : g.Bcol[csel - 1];
+  void* Cw = csel == 0 ? g.C : g.Ccol[csel - 1];
 
   // Global-load assignment.
   // A: vector v = tid + j*256 -> row v/8, k-chunk v%8.
@@ -203,9 +216,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
       const int gn = n0 + (BT ? v % (BN / 8) : b_nc) * 8;
       const int gk = k0 + kr;
       b_ok[P][r] = gk < kend && gn < g.N;
-      const int64_t off = static_cast<int64_t>(min(kl + kr, g.K - 1)) * g.N + min(gn, g.N - 8);
+      const int64_t off = static_cast<int64_t>(min(kl + kr, g.K - 1)) * ldbc + min(gn - ncol0, ldbc - 8);
 #pragma unroll
-      for (int q = 0; q < NB; ++q) b_raw[P][q][r] = load_vec((q == 0 ? g.B : g.B2) + off);
+      for (int q = 0; q < NB; ++q) b_raw[P][q][r] = load_vec((q == 0 ? Bw : g.B2) + off);
     }
   };
 
@@ -493,12 +506,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   };
 
   auto write_out = [&](int gm, int gn, float v0, float v1) {
+    const int64_t o = static_cast<int64_t>(gm) * ldbc + (gn - ncol0);
     if constexpr (EPI == kSiluMul) {
-      static_cast<float*>(g.C)[static_cast<int64_t>(gm) * g.N + gn] = silu(v0) * v1;
+      static_cast<float*>(Cw)[o] = silu(v0) * v1;
     } else {
       (void)v1;
-      if (EPI == kPlain && g.c_f32) static_cast<float*>(g.C)[static_cast<int64_t>(gm) * g.N + gn] = v0;
-      else static_cast<bf16*>(g.C)[static_cast<int64_t>(gm) * g.N + gn] = static_cast<bf16>(v0);
+      if (EPI == kPlain && g.c_f32) static_cast<float*>(Cw)[o] = v0;
+      else static_cast<bf16*>(Cw)[o] = static_cast<bf16>(v0);
     }
   };
 
@@ -614,6 +628,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) 
   }
   float sc = 1.f;
   (void)BN;
+  // Output block of a column-split C (a quad never straddles: ncol % 8 == 0).
+  const int csel = g.ncol > 0 ? gn / g.ncol : 0;
+  void* Cw = csel == 0 ? g.C : g.Ccol[csel - 1];
+  const int64_t oidx = g.ncol > 0 ? static_cast<int64_t>(gm) * g.ncol + (gn - csel * g.ncol) : idx;
   if constexpr (RMS) sc = row_scale[gm - static_cast<int>(static_cast<int64_t>(blockIdx.x) * blockDim.x * 4 / g.N)];
   if constexpr (EPI == kPlain) {
     if (g.rscale != nullptr) sc = g.rscale[gm];
@@ -622,18 +640,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) 
     Vec<float> o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o.v[e] = silu(v[0][e]) * v[1][e];
-    store_vec(static_cast<float*>(g.C) + idx, o);
+    store_vec(static_cast<float*>(Cw) + oidx, o);
   } else if (EPI == kPlain && g.c_f32) {
     Vec<float> o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o.v[e] = v[0][e] * sc;
-    store_vec(static_cast<float*>(g.C) + idx, o);
+    store_vec(static_cast<float*>(Cw) + oidx, o);
   } else {
     typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
     bf16x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(v[0][e] * sc);
-    *reinterpret_cast<bf16x4*>(static_cast<bf16*>(g.C) + idx) = o;
+    *reinterpret_cast<bf16x4*>(static_cast<bf16*>(Cw) + oidx) = o;
   }
 }
 
@@ -1732,8 +1750,16 @@ const char* summary_la(int variant) {
 // TILES_IN_BLOCK_P = columns / 64 of S, TILES_IN_BLOCK_K = K range / 256 of
 // every stage. The output stage holds two A planes, so its tile is narrowed
 // to BM <= 128 and BM x BN <= 128 x 128.
+// The three projections run as one GEMM over the column-split operand
+// [w_q | w_k | w_v] (x read once, one launch, one split-K fixup) whenever
+// the projection tile width divides n; otherwise as three GEMMs. The merged
+// GEMM takes the fewest K splits (powers of two) that give it at least 128
+// workgroups, whatever TILES_IN_BLOCK_K says: its partials are three times
+// those of one projection, and at 4096 x 1536 x 4096 two splits (192
+// workgroups) run in 76 us where four take 97.
 struct AttnPlan {
-  Plan proj, s, pv;
+  Plan proj, proj3, s, pv;
+  bool merged;
 };
 
 AttnPlan attn_plan(const Call& c) {
@@ -1742,6 +1768,17 @@ AttnPlan attn_plan(const Call& c) {
   const int tm2 = std::min(tm, 2), tn2 = std::max(1, std::min(tn, 4 / tm2));
   AttnPlan P;
   P.proj = plan_of(m, n, k, tm, tn, tk);
+  {
+    int tk_full = 1;  // K range covering all of k, in units of kKUnit
+    while (static_cast<int64_t>(kKUnit) * tk_full < k) tk_full *= 2;
+    int tk3 = tk_full;
+    const Plan whole = plan_of(m, 3 * n, k, tm, tn, tk_full);
+    for (int splits = 1; tk3 > 1 && static_cast<int64_t>(whole.MT) * whole.NT * splits < 128; splits *= 2) tk3 /= 2;
+    P.proj3 = plan_of(m, 3 * n, k, tm, tn, tk3);
+  }
+  std::string why;
+  P.merged = n > 0 && n % P.proj3.BN == 0 &&
+             check_gemm_shape(m, 3 * static_cast<int64_t>(n), k, tm, tn, tk, &why) == AXON_OK;
   P.s = plan_of(m, m, n, tm, tp, tk);
   P.pv = plan_of(m, n, m, tm2, tn2, tk);
   return P;
@@ -1799,7 +1836,8 @@ AttnLayout attn_layout(const Call& c) {
   L.kt = 3 * mn;
   L.s = 4 * mn;
   L.data = L.s + align256(static_cast<size_t>(m) * m * sizeof(float));
-  const size_t d = std::max({data_bytes(L.P.proj, m, n, 1), data_bytes(L.P.s, m, m, 1), data_bytes(L.P.pv, m, n, 1)});
+  const size_t dproj = L.P.merged ? data_bytes(L.P.proj3, m, 3 * n, 1) : data_bytes(L.P.proj, m, n, 1);
+  const size_t d = std::max({dproj, data_bytes(L.P.s, m, m, 1), data_bytes(L.P.pv, m, n, 1)});
   L.total = L.data + d;
   return L;
 }
@@ -1832,10 +1870,20 @@ int launch_attn_qkv(const Call& c, const void* const* in, void* const* out, void
   void* data = base + L.data;
   bf16* proj_out[3] = {q, kk, v};
   int rc = AXON_OK;
-  for (int i = 0; i < 3 && rc == AXON_OK; ++i) {
-    const GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[1 + i]), nullptr, proj_out[i], m, n, k,
-                                 L.P.proj, data, 1, 0.f);
-    rc = dispatch<kPlain, false>(L.P.proj.BM, L.P.proj.BN, g, st, c.variant);
+  if (L.P.merged) {
+    GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[1]), nullptr, q, m, 3 * n, k, L.P.proj3, data, 1, 0.f);
+    g.Bcol[0] = static_cast<const bf16*>(in[2]);
+    g.Bcol[1] = static_cast<const bf16*>(in[3]);
+    g.Ccol[0] = kk;
+    g.Ccol[1] = v;
+    g.ncol = n;
+    rc = dispatch<kPlain, false>(L.P.proj3.BM, L.P.proj3.BN, g, st, c.variant);
+  } else {
+    for (int i = 0; i < 3 && rc == AXON_OK; ++i) {
+      const GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[1 + i]), nullptr, proj_out[i], m, n, k,
+                                   L.P.proj, data, 1, 0.f);
+      rc = dispatch<kPlain, false>(L.P.proj.BM, L.P.proj.BN, g, st, c.variant);
+    }
   }
   if (rc == AXON_OK) rc = launch_transpose(kk, kt, m, n, st);
   if (rc != AXON_OK) return rc;
