@@ -5,7 +5,7 @@ Reads either the SQLite database rocprofv3 writes by default
 `--stats --output-format csv`, and prints a Markdown table: calls, average,
 min and max duration per kernel, sorted by total time.
 
-    python -m enzyme_amd.rocprof_summary gpurun_out/prof_bench/bench_results.db
+    python -m enzyme_amd.rocprof_summary prof/bench_results.db
 """
 
 from __future__ import annotations

@@ -19,12 +19,12 @@ Two subcommands:
 Example (on the GPU host, from the repository root):
 
     cd /tmp && export TMPDIR=/tmp
-    rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_fetch -o fetch \\
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/prof/pmc_fetch -o fetch \\
         -- python3 $R/enzyme_amd/traffic.py run rope_llama3
-    rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_write -o write \\
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/prof/pmc_write -o write \\
         -- python3 $R/enzyme_amd/traffic.py run rope_llama3
     python3 $R/enzyme_amd/traffic.py summarize rope_llama3 \\
-        --fetch $R/gpurun_out/pmc_fetch --write $R/gpurun_out/pmc_write --out $R/profiles
+        --fetch $R/prof/pmc_fetch --write $R/prof/pmc_write --out $R/profiles
 """
 
 from __future__ import annotations
