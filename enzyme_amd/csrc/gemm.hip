@@ -1748,8 +1748,10 @@ const char* summary_la(int variant) {
 // Tiles: TILES_IN_BLOCK_M = rows per tile / 64 (all stages),
 // TILES_IN_BLOCK_N = columns / 64 of the projections and of the output,
 // TILES_IN_BLOCK_P = columns / 64 of S, TILES_IN_BLOCK_K = K range / 256 of
-// every stage. The output stage holds two A planes, so its tile is narrowed
-// to BM <= 128 and BM x BN <= 128 x 128.
+// the S stage (and of the projections when they run as three GEMMs; the
+// merged projection and the output stage pick their own, below). The output
+// stage holds two A planes, so its tile is narrowed to BM <= 128 and
+// BM x BN <= 128 x 128.
 // The three projections run as one GEMM over the column-split operand
 // [w_q | w_k | w_v] (x read once, one launch, one split-K fixup) whenever
 // the projection tile width divides n; otherwise as three GEMMs. The merged
@@ -1780,7 +1782,18 @@ AttnPlan attn_plan(const Call& c) {
   P.merged = n > 0 && n % P.proj3.BN == 0 &&
              check_gemm_shape(m, 3 * static_cast<int64_t>(n), k, tm, tn, tk, &why) == AXON_OK;
   P.s = plan_of(m, m, n, tm, tp, tk);
-  P.pv = plan_of(m, n, m, tm2, tn2, tk);
+  // The softmax GEMM likewise takes the fewest K splits that give it at
+  // least 256 workgroups (4096 x 512 x 4096 on 128 x 128 tiles: two splits,
+  // 16 MB of partials, where TILES_IN_BLOCK_K = 2 would make eight and 64 MB;
+  // s4k_d512 230 -> 206 us; a 128-workgroup floor is slower here).
+  {
+    int tk_full = 1;
+    while (static_cast<int64_t>(kKUnit) * tk_full < m) tk_full *= 2;
+    int tkp = tk_full;
+    const Plan whole = plan_of(m, n, m, tm2, tn2, tk_full);
+    for (int splits = 1; tkp > 1 && static_cast<int64_t>(whole.MT) * whole.NT * splits < 256; splits *= 2) tkp /= 2;
+    P.pv = plan_of(m, n, m, tm2, tn2, tkp);
+  }
   return P;
 }
 
