@@ -73,7 +73,10 @@ constexpr int kXcds = 8;
 // loaded), with the kRmsEps row scale taken over that sum.
 // kSoftmax: A is replaced by exp(A) as loaded (fp32), and the output row is
 // scaled by 1 / sum_k exp(A): softmax without max subtraction, then @ B.
-enum Epi { kPlain = 0, kRmsSum = 1, kRmsEps = 2, kSiluMul = 3, kQkv = 4, kSoftmax = 5 };
+// kColSplit: the plain product with column-split operands (GemmArgs::Bcol,
+// Ccol, ncol); a separate instantiation so the other epilogues keep their
+// register allocation.
+enum Epi { kPlain = 0, kRmsSum = 1, kRmsEps = 2, kSiluMul = 3, kQkv = 4, kSoftmax = 5, kColSplit = 6 };
 
 // Epilogues that scale each output row by a statistic of its A row, summed
 // over K as the A tiles are staged (squares for the RMS forms, the values
@@ -96,10 +99,10 @@ struct GemmArgs {
   int S, MT, NT;
   float eps;
   int c_f32;            // kPlain: C is fp32 instead of bf16
-  // Column-split operands (kPlain, hw variants 0/1): with ncol > 0 the
-  // logical B [K, N] is [B | Bcol[0] | Bcol[1]] and C [M, N] is
-  // [C | Ccol[0] | Ccol[1]], each block ncol columns wide and contiguous on
-  // its own (N = 3 ncol, ncol a multiple of BN, so a tile never straddles).
+  // Column-split operands (kColSplit, hw variants 0/1): the logical B [K, N]
+  // is [B | Bcol[0] | Bcol[1]] and C [M, N] is [C | Ccol[0] | Ccol[1]], each
+  // block ncol columns wide and contiguous on its own (N = 3 ncol, ncol a
+  // multiple of BN, so a tile never straddles two).
   const bf16* Bcol[2];
   void* Ccol[2];
   int ncol;
@@ -147,11 +150,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   const int kbeg = z * g.kchunk;
   const int kend = min(g.K, kbeg + g.kchunk);
   // This tile's B and C blocks (the whole of B and C unless column-split).
-  const int csel = g.ncol > 0 ? n0 / g.ncol : 0;
-  const int ncol0 = csel * g.ncol;
-  const int ldbc = g.ncol > 0 ? g.ncol : g.N;
-  const bf16* Bw = csel == 0 ? g.B : g.Bcol[csel - 1];
-  void* Cw = csel == 0 ? g.C : g.Ccol[csel - 1];
+  constexpr bool CS = EPI == kColSplit;
+  const int csel = CS ? n0 / g.ncol : 0;
+  const int ncol0 = CS ? csel * g.ncol : 0;
+  const int ldbc = CS ? g.ncol : g.N;
+  const bf16* Bw = CS && csel > 0 ? g.Bcol[csel - 1] : g.B;
+  void* Cw = CS && csel > 0 ? g.Ccol[csel - 1] : g.C;
 
   // Global-load assignment.
   // A: vector v = tid + j*256 -> row v/8, k-chunk v%8.
@@ -629,9 +633,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) 
   float sc = 1.f;
   (void)BN;
   // Output block of a column-split C (a quad never straddles: ncol % 8 == 0).
-  const int csel = g.ncol > 0 ? gn / g.ncol : 0;
-  void* Cw = csel == 0 ? g.C : g.Ccol[csel - 1];
-  const int64_t oidx = g.ncol > 0 ? static_cast<int64_t>(gm) * g.ncol + (gn - csel * g.ncol) : idx;
+  constexpr bool CS = EPI == kColSplit;
+  const int csel = CS ? gn / g.ncol : 0;
+  void* Cw = CS && csel > 0 ? g.Ccol[csel - 1] : g.C;
+  const int64_t oidx = CS ? static_cast<int64_t>(gm) * g.ncol + (gn - csel * g.ncol) : idx;
   if constexpr (RMS) sc = row_scale[gm - static_cast<int>(static_cast<int64_t>(blockIdx.x) * blockDim.x * 4 / g.N)];
   if constexpr (EPI == kPlain) {
     if (g.rscale != nullptr) sc = g.rscale[gm];
@@ -1890,7 +1895,7 @@ int launch_attn_qkv(const Call& c, const void* const* in, void* const* out, void
     g.Ccol[0] = kk;
     g.Ccol[1] = v;
     g.ncol = n;
-    rc = dispatch<kPlain, false>(L.P.proj3.BM, L.P.proj3.BN, g, st, c.variant);
+    rc = dispatch<kColSplit, false>(L.P.proj3.BM, L.P.proj3.BN, g, st, c.variant);
   } else {
     for (int i = 0; i < 3 && rc == AXON_OK; ++i) {
       const GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[1 + i]), nullptr, proj_out[i], m, n, k,
