@@ -224,8 +224,8 @@ def main(argv=None) -> int:
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(
-            f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every path here runs "
-            "on one MI355X; how each would shard is described in DESIGN.md)",
+            f"bench.py measures one GPU; --gpus {args.gpus} is not supported: every kernel here runs "
+            "on one MI355X, and no multi-GPU figure is produced",
             file=sys.stderr,
         )
         return 2
