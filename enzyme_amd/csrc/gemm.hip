@@ -113,6 +113,14 @@ __device__ __forceinline__ float silu(float a) { return a / (1.f + __expf(-a)); 
 template <int N>
 using ic = std::integral_constant<int, N>;
 
+// The fused residual-sum epilogue at prefetch depth 1 runs the rolling
+// refill with sliced compute (gemm_kernel's step); its B is staged as loaded
+// and read with the transposing LDS read, like every deeper pipeline.
+template <int EPI, int PD>
+constexpr bool rolling() { return EPI == kQkv && PD == 1; }
+template <int EPI, int PD>
+constexpr bool b_transposed() { return PD > 1 || rolling<EPI, PD>(); }
+
 template <int BM, int BN, int EPI, bool A_F32, int PD>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   constexpr bool DUAL = EPI == kSiluMul;
@@ -128,7 +136,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   // B is staged transposed ([n][k], pitch LDK) with one register set (hw
   // variant 0), or as loaded ([k][n], pitch PB) and read with the
   // transposing LDS read (several register sets, hw variant 1).
-  constexpr bool BT = PD > 1;
+  constexpr bool BT = b_transposed<EPI, PD>();
+  constexpr bool ROLL = rolling<EPI, PD>();
   constexpr int PB = bpitch(BN);
   bf16* As = reinterpret_cast<bf16*>(smem);                 // [2][NA][BM][LDK]
   bf16* Bs = As + 2 * NA * BM * LDK;                        // [2][NB][BN][LDK] or [2][NB][BK][PB]
@@ -188,11 +197,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   // the compiler's memory-counter waits stay exact.
   const int klast = kbeg + max(nsteps - 1, 0) * BK;
 
-  auto load_global = [&](int k0, auto set_tag) {
+  // Loads of A vector j (AW 16-byte loads) and of the whole B block for the
+  // K step at k0 into register set P.
+  auto load_a = [&](int k0, auto set_tag, int j) {
     constexpr int P = decltype(set_tag)::value;
     const int kl = min(k0, klast);
-#pragma unroll
-    for (int j = 0; j < AV; ++j) {
+    {
       const int v = tid + j * kThreads;
       const int r = v >> 3, kc = (v & 7) * 8;
       const int gm = m0 + r, gk = k0 + kc;
@@ -210,6 +220,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         }
       }
     }
+  };
+  auto load_b = [&](int k0, auto set_tag) {
+    constexpr int P = decltype(set_tag)::value;
+    const int kl = min(k0, klast);
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
       // Variant 0: rows b_kb*KR + r of column chunk b_nc. Variant 1: vector
@@ -225,15 +239,18 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
       for (int q = 0; q < NB; ++q) b_raw[P][q][r] = load_vec((q == 0 ? Bw : g.B2) + off);
     }
   };
+  auto load_global = [&](int k0, auto set_tag) {
+#pragma unroll
+    for (int j = 0; j < AV; ++j) load_a(k0, set_tag, j);
+    load_b(k0, set_tag);
+  };
 
-  auto store_lds = [&](int buf, auto set_tag) {
+  // LDS stores of A vector j and of the B block from register set P.
+  auto store_a = [&](int buf, auto set_tag, int j) {
     constexpr int P = decltype(set_tag)::value;
     auto& a_raw_p = a_raw[P];
     auto& a_ok_p = a_ok[P];
-    auto& b_raw_p = b_raw[P];
-    auto& b_ok_p = b_ok[P];
-#pragma unroll
-    for (int j = 0; j < AV; ++j) {
+    {
       const int v = tid + j * kThreads;
       const int r = v >> 3, kc = (v & 7) * 8;
       float x[8];
@@ -299,6 +316,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         for (int e = 0; e < 8; ++e) sq[j] += x[e] * x[e];
       }
     }
+  };
+  auto store_b = [&](int buf, auto set_tag) {
+    constexpr int P = decltype(set_tag)::value;
+    auto& b_raw_p = b_raw[P];
+    auto& b_ok_p = b_ok[P];
     if constexpr (BT) {
 #pragma unroll
       for (int q = 0; q < NB; ++q)
@@ -352,6 +374,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         }
       }
     }
+  };
+  auto store_lds = [&](int buf, auto set_tag) {
+#pragma unroll
+    for (int j = 0; j < AV; ++j) store_a(buf, set_tag, j);
+    store_b(buf, set_tag);
   };
 
   floatx16 acc[NB][TM][TN];
@@ -408,6 +435,38 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     }
   };
 
+  // compute() cut into slices for the rolling refill: MFMA unit u covers
+  // (kk = u / TN, B column tile u % TN); the A fragments of a kk are read at
+  // its first unit and kept until its last.
+  bf16x8 af_s[TM];
+  auto compute_units = [&](int buf, int u0, int u1) {
+    static_assert(!ROLL || (NA == 1 && NB == 1), "sliced compute covers the single-plane, single-B case");
+#pragma unroll
+    for (int u = u0; u < u1; ++u) {
+      const int kk = u / TN, jn = u % TN;
+      const int kof = kk * 16 + (lane >> 5) * 8;
+      if (jn == 0) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          af_s[i] = *reinterpret_cast<const bf16x8*>(As + (buf * BM + wm * WM + i * 32 + (lane & 31)) * LDK + kof);
+      }
+      bf16x8 bfr;
+      if constexpr (BT) {
+        const int g4 = lane >> 4, s16 = lane & 15;
+        const int nb = wn * WN + jn * 32 + 16 * (g4 & 1);
+        const int kr0 = kk * 16 + 8 * (g4 >> 1) + (s16 >> 2);
+        const bf16* bp = Bs + (buf * BK + kr0) * PB + nb + 4 * (s16 & 3);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp + 4 * PB));
+        bfr = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      } else {
+        bfr = *reinterpret_cast<const bf16x8*>(Bs + (buf * BN + wn * WN + jn * 32 + (lane & 31)) * LDK + kof);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) acc[0][i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af_s[i], bfr, acc[0][i][jn], 0, 0, 0);
+    }
+  };
+
   // Pipeline: K steps 0..PD-1 are loaded up front; after step s is computed
   // from LDS buffer s&1, step s+1 moves from its register set into the other
   // buffer and that set is refilled with step s+1+PD. Full groups of PD steps
@@ -418,8 +477,24 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     if constexpr (PD > 1) load_global(kbeg + BK, ic<1>{});
     if constexpr (PD > 2) load_global(kbeg + 2 * BK, ic<2>{});
     if constexpr (PD > 3) load_global(kbeg + 3 * BK, ic<3>{});
-    store_lds(0, ic<0>{});
-    load_global(kbeg + PD * BK, ic<0>{});
+    if constexpr (ROLL) {
+      // Same store/refill order as the loop body, so the loads in flight at
+      // the loop entry are those the loop's waits are counted against.
+#pragma unroll
+      for (int j = 0; j < AV; ++j) {
+        store_a(0, ic<0>{}, j);
+        __builtin_amdgcn_sched_barrier(0);
+        load_a(kbeg + PD * BK, ic<0>{}, j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      store_b(0, ic<0>{});
+      __builtin_amdgcn_sched_barrier(0);
+      load_b(kbeg + PD * BK, ic<0>{});
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      store_lds(0, ic<0>{});
+      load_global(kbeg + PD * BK, ic<0>{});
+    }
   }
   __syncthreads();
   // Global loads and MFMAs per K step (for the load/MFMA interleave).
@@ -434,6 +509,29 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     constexpr int J = decltype(j_tag)::value;
     constexpr int NX = (J + 1) % PD;  // register set of step s + 1
     const int s = s0 + J;
+    if constexpr (ROLL) {
+      // Each vector's refill is issued as soon as its store has read the
+      // registers, so the next step's loads start during this store phase
+      // instead of after it.
+      // Slice j of this step's MFMAs goes with the store and refill of A
+      // vector j: the MFMAs run while the conversion VALU work and the load
+      // waits of the slice are issued (the two touch different LDS buffers).
+      constexpr int U = (BK / 16) * TN;
+#pragma unroll
+      for (int j = 0; j < AV; ++j) {
+        compute_units(s & 1, j * U / AV, (j + 1) * U / AV);
+        store_a((s + 1) & 1, ic<NX>{}, j);
+        __builtin_amdgcn_sched_barrier(0);
+        load_a(kbeg + (s + 1 + PD) * BK, ic<NX>{}, j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      store_b((s + 1) & 1, ic<NX>{});
+      __builtin_amdgcn_sched_barrier(0);
+      load_b(kbeg + (s + 1 + PD) * BK, ic<NX>{});
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+      return;
+    }
     store_lds((s + 1) & 1, ic<NX>{});
     // The refill reuses the registers the stores just read: issued earlier,
     // it would need other registers and copies that wait for loads in flight.
@@ -1088,7 +1186,7 @@ size_t gemm_workspace(int M, int N, int K, int tm, int tn, int tk, int nb) {
 template <int BM, int BN, int EPI, bool AF, int PD>
 void launch_tile(const GemmArgs& g, hipStream_t st) {
   constexpr int na = AF ? 2 : 1, nb = EPI == kSiluMul ? 2 : 1;
-  const size_t lds = lds_bytes(BM, BN, na, nb, PD > 1);
+  const size_t lds = lds_bytes(BM, BN, na, nb, b_transposed<EPI, PD>());
   auto fn = gemm_kernel<BM, BN, EPI, AF, PD>;
   // Raising the dynamic LDS limit is idempotent, so a race between threads
   // doing it for the first time is harmless.
