@@ -13,11 +13,17 @@
 // Schedule (hw variant 0): a workgroup of 4 waves (2 x 2) owns a BM x BN
 // output tile and a K range of 64*TK. Per 64-deep K step it loads the A tile
 // (16-byte vectors along K) and the B tile (16-byte vectors along N) into
-// registers, stores A to LDS as is and B transposed (each thread turns KR
-// rows x 8 columns into 8 rows of KR k-values), so both MFMA operands are
-// read from LDS as 16-byte k-runs. The next step's global loads are issued
-// before the current step's MFMAs (v_mfma_f32_32x32x16_bf16), so HBM latency
-// hides behind the matrix cores; LDS is double-buffered.
+// one register set and stores both to the LDS buffer the MFMAs
+// (v_mfma_f32_32x32x16_bf16) do not read; LDS is double-buffered. With one A
+// plane and one B operand (bf16 A, every epilogue but silu_mlp's) the step
+// is a rolling refill: A vector j is stored and at once reloaded for the
+// step after next, and the step's MFMAs are cut into slices issued between
+// those stores, so the matrix cores run under the staging work and the load
+// waits; B is stored as loaded ([k][n]) and its MFMA fragments come from the
+// transposing LDS read (below). fp32 A (hi/lo planes) and silu_mlp's two B
+// operands keep the plain order (all stores, refill, then the MFMAs) with B
+// transposed in registers (each thread turns KR rows x 8 columns into 8 rows
+// of KR k-values).
 // The RMSNorm row scale needs sum_k A^2: each thread accumulates the squares
 // of the A vectors it already holds, so A is read once.
 // Split K (K range < K): each workgroup writes its fp32 partial tile (and its
@@ -113,13 +119,14 @@ __device__ __forceinline__ float silu(float a) { return a / (1.f + __expf(-a)); 
 template <int N>
 using ic = std::integral_constant<int, N>;
 
-// The fused residual-sum epilogue at prefetch depth 1 runs the rolling
-// refill with sliced compute (gemm_kernel's step); its B is staged as loaded
-// and read with the transposing LDS read, like every deeper pipeline.
-template <int EPI, int PD>
-constexpr bool rolling() { return EPI == kQkv && PD == 1; }
-template <int EPI, int PD>
-constexpr bool b_transposed() { return PD > 1 || rolling<EPI, PD>(); }
+// Prefetch depth 1 with one A plane and one B operand (every epilogue but
+// kSiluMul, bf16 A) runs the rolling refill with sliced compute
+// (gemm_kernel's step); its B is staged as loaded and read with the
+// transposing LDS read, like every deeper pipeline.
+template <int EPI, int PD, bool AF>
+constexpr bool rolling() { return !AF && EPI != kSiluMul && PD == 1; }
+template <int EPI, int PD, bool AF>
+constexpr bool b_transposed() { return PD > 1 || rolling<EPI, PD, AF>(); }
 
 template <int BM, int BN, int EPI, bool A_F32, int PD>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
@@ -136,8 +143,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   // B is staged transposed ([n][k], pitch LDK) with one register set (hw
   // variant 0), or as loaded ([k][n], pitch PB) and read with the
   // transposing LDS read (several register sets, hw variant 1).
-  constexpr bool BT = b_transposed<EPI, PD>();
-  constexpr bool ROLL = rolling<EPI, PD>();
+  constexpr bool BT = b_transposed<EPI, PD, A_F32>();
+  constexpr bool ROLL = rolling<EPI, PD, A_F32>();
   constexpr int PB = bpitch(BN);
   bf16* As = reinterpret_cast<bf16*>(smem);                 // [2][NA][BM][LDK]
   bf16* Bs = As + 2 * NA * BM * LDK;                        // [2][NB][BN][LDK] or [2][NB][BK][PB]
@@ -1186,7 +1193,7 @@ size_t gemm_workspace(int M, int N, int K, int tm, int tn, int tk, int nb) {
 template <int BM, int BN, int EPI, bool AF, int PD>
 void launch_tile(const GemmArgs& g, hipStream_t st) {
   constexpr int na = AF ? 2 : 1, nb = EPI == kSiluMul ? 2 : 1;
-  const size_t lds = lds_bytes(BM, BN, na, nb, b_transposed<EPI, PD>());
+  const size_t lds = lds_bytes(BM, BN, na, nb, b_transposed<EPI, PD, AF>());
   auto fn = gemm_kernel<BM, BN, EPI, AF, PD>;
   // Raising the dynamic LDS limit is idempotent, so a race between threads
   // doing it for the first time is harmless.
@@ -1433,11 +1440,13 @@ const char* summary_mm(int variant) {
            "K ranges; needs k % 64 == 0";
   return variant == 1
              ? "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, 2-3 K steps of global loads in flight in "
-               "rotating register sets, LDS double buffer with B transposed on store, split-K with a "
-               "parallel fixup kernel, XCD-grouped K ranges, fused row-scale epilogue"
-             : "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, LDS double buffer with B transposed on "
-               "store, split-K with a parallel fixup kernel, XCD-grouped K ranges, fused row-scale "
-               "epilogue";
+               "rotating register sets, LDS double buffer with B staged as loaded and read by the "
+               "transposing LDS read, split-K with a parallel fixup kernel, XCD-grouped K ranges, fused "
+               "row-scale epilogue"
+             : "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, one K step of loads in flight refilled "
+               "vector by vector with the MFMAs sliced between the A stores (fp32 inputs: all stores, "
+               "then the MFMAs, B transposed on store), LDS double buffer, split-K with a parallel "
+               "fixup kernel, XCD-grouped K ranges, fused row-scale epilogue";
 }
 
 // ---- silu_mlp (dims m, n, k, p; x[m,k], w1[k,n], w2[k,n], w3[n,p]) --------
