@@ -14,16 +14,16 @@
 // output tile and a K range of 64*TK. Per 64-deep K step it loads the A tile
 // (16-byte vectors along K) and the B tile (16-byte vectors along N) into
 // one register set and stores both to the LDS buffer the MFMAs
-// (v_mfma_f32_32x32x16_bf16) do not read; LDS is double-buffered. With one A
-// plane and one B operand (bf16 A, every epilogue but silu_mlp's) the step
-// is a rolling refill: A vector j is stored and at once reloaded for the
-// step after next, and the step's MFMAs are cut into slices issued between
-// those stores, so the matrix cores run under the staging work and the load
-// waits; B is stored as loaded ([k][n]) and its MFMA fragments come from the
-// transposing LDS read (below). fp32 A (hi/lo planes) and silu_mlp's two B
-// operands keep the plain order (all stores, refill, then the MFMAs) with B
-// transposed in registers (each thread turns KR rows x 8 columns into 8 rows
-// of KR k-values).
+// (v_mfma_f32_32x32x16_bf16) do not read; LDS is double-buffered. With one
+// B operand (every epilogue but silu_mlp's) the step is a rolling refill: A
+// vector j is stored and at once reloaded for the step after next, and the
+// step's MFMAs are cut into slices issued between those stores, so the
+// matrix cores run under the staging work (fp32 A: exp, hi/lo split) and
+// the load waits; B is stored as loaded ([k][n]) and its MFMA fragments come
+// from the transposing LDS read (below). silu_mlp's two B operands keep the
+// plain order (all stores, refill, then the MFMAs) with B transposed in
+// registers (each thread turns KR rows x 8 columns into 8 rows of KR
+// k-values).
 // The RMSNorm row scale needs sum_k A^2: each thread accumulates the squares
 // of the A vectors it already holds, so A is read once.
 // Split K (K range < K): each workgroup writes its fp32 partial tile (and its
@@ -119,12 +119,12 @@ __device__ __forceinline__ float silu(float a) { return a / (1.f + __expf(-a)); 
 template <int N>
 using ic = std::integral_constant<int, N>;
 
-// Prefetch depth 1 with one A plane and one B operand (every epilogue but
-// kSiluMul, bf16 A) runs the rolling refill with sliced compute
-// (gemm_kernel's step); its B is staged as loaded and read with the
-// transposing LDS read, like every deeper pipeline.
+// Prefetch depth 1 with one B operand (every epilogue but kSiluMul) runs the
+// rolling refill with sliced compute (gemm_kernel's step); its B is staged
+// as loaded and read with the transposing LDS read, like every deeper
+// pipeline.
 template <int EPI, int PD, bool AF>
-constexpr bool rolling() { return !AF && EPI != kSiluMul && PD == 1; }
+constexpr bool rolling() { return EPI != kSiluMul && PD == 1; }
 template <int EPI, int PD, bool AF>
 constexpr bool b_transposed() { return PD > 1 || rolling<EPI, PD, AF>(); }
 
@@ -445,17 +445,20 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   // compute() cut into slices for the rolling refill: MFMA unit u covers
   // (kk = u / TN, B column tile u % TN); the A fragments of a kk are read at
   // its first unit and kept until its last.
-  bf16x8 af_s[TM];
+  bf16x8 af_s[NA][TM];
   auto compute_units = [&](int buf, int u0, int u1) {
-    static_assert(!ROLL || (NA == 1 && NB == 1), "sliced compute covers the single-plane, single-B case");
+    static_assert(!ROLL || NB == 1, "sliced compute covers the single-B case");
 #pragma unroll
     for (int u = u0; u < u1; ++u) {
       const int kk = u / TN, jn = u % TN;
       const int kof = kk * 16 + (lane >> 5) * 8;
       if (jn == 0) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          af_s[i] = *reinterpret_cast<const bf16x8*>(As + (buf * BM + wm * WM + i * 32 + (lane & 31)) * LDK + kof);
+        for (int p = 0; p < NA; ++p)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+            af_s[p][i] = *reinterpret_cast<const bf16x8*>(
+                As + ((buf * NA + p) * BM + wm * WM + i * 32 + (lane & 31)) * LDK + kof);
       }
       bf16x8 bfr;
       if constexpr (BT) {
@@ -470,7 +473,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         bfr = *reinterpret_cast<const bf16x8*>(Bs + (buf * BN + wn * WN + jn * 32 + (lane & 31)) * LDK + kof);
       }
 #pragma unroll
-      for (int i = 0; i < TM; ++i) acc[0][i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af_s[i], bfr, acc[0][i][jn], 0, 0, 0);
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int p = 0; p < NA; ++p)
+          acc[0][i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af_s[p][i], bfr, acc[0][i][jn], 0, 0, 0);
     }
   };
 
@@ -1444,9 +1450,9 @@ const char* summary_mm(int variant) {
                "transposing LDS read, split-K with a parallel fixup kernel, XCD-grouped K ranges, fused "
                "row-scale epilogue"
              : "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, one K step of loads in flight refilled "
-               "vector by vector with the MFMAs sliced between the A stores (fp32 inputs: all stores, "
-               "then the MFMAs, B transposed on store), LDS double buffer, split-K with a parallel "
-               "fixup kernel, XCD-grouped K ranges, fused row-scale epilogue";
+               "vector by vector with the MFMAs sliced between the A stores, LDS double buffer with B "
+               "staged as loaded, split-K with a parallel fixup kernel, XCD-grouped K ranges, fused "
+               "row-scale epilogue";
 }
 
 // ---- silu_mlp (dims m, n, k, p; x[m,k], w1[k,n], w2[k,n], w3[n,p]) --------
