@@ -14,16 +14,13 @@
 // output tile and a K range of 64*TK. Per 64-deep K step it loads the A tile
 // (16-byte vectors along K) and the B tile (16-byte vectors along N) into
 // one register set and stores both to the LDS buffer the MFMAs
-// (v_mfma_f32_32x32x16_bf16) do not read; LDS is double-buffered. With one
-// B operand (every epilogue but silu_mlp's) the step is a rolling refill: A
-// vector j is stored and at once reloaded for the step after next, and the
-// step's MFMAs are cut into slices issued between those stores, so the
-// matrix cores run under the staging work (fp32 A: exp, hi/lo split) and
-// the load waits; B is stored as loaded ([k][n]) and its MFMA fragments come
-// from the transposing LDS read (below). silu_mlp's two B operands keep the
-// plain order (all stores, refill, then the MFMAs) with B transposed in
-// registers (each thread turns KR rows x 8 columns into 8 rows of KR
-// k-values).
+// (v_mfma_f32_32x32x16_bf16) do not read; LDS is double-buffered. The step
+// is a rolling refill: A vector j is stored and at once reloaded for the
+// step after next, and the step's MFMAs are cut into slices issued between
+// those stores, so the matrix cores run under the staging work (fp32 A:
+// exp, hi/lo split) and the load waits; B (both operands for silu_mlp) is
+// stored as loaded ([k][n]) and its MFMA fragments come from the
+// transposing LDS read (below).
 // The RMSNorm row scale needs sum_k A^2: each thread accumulates the squares
 // of the A vectors it already holds, so A is read once.
 // Split K (K range < K): each workgroup writes its fp32 partial tile (and its
@@ -119,12 +116,11 @@ __device__ __forceinline__ float silu(float a) { return a / (1.f + __expf(-a)); 
 template <int N>
 using ic = std::integral_constant<int, N>;
 
-// Prefetch depth 1 with one B operand (every epilogue but kSiluMul) runs the
-// rolling refill with sliced compute (gemm_kernel's step); its B is staged
-// as loaded and read with the transposing LDS read, like every deeper
-// pipeline.
+// Prefetch depth 1 (hw variant 0, every epilogue) runs the rolling refill
+// with sliced compute (gemm_kernel's step); its B is staged as loaded and
+// read with the transposing LDS read, like every deeper pipeline.
 template <int EPI, int PD, bool AF>
-constexpr bool rolling() { return EPI != kSiluMul && PD == 1; }
+constexpr bool rolling() { return PD == 1; }
 template <int EPI, int PD, bool AF>
 constexpr bool b_transposed() { return PD > 1 || rolling<EPI, PD, AF>(); }
 
@@ -447,7 +443,6 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   // its first unit and kept until its last.
   bf16x8 af_s[NA][TM];
   auto compute_units = [&](int buf, int u0, int u1) {
-    static_assert(!ROLL || NB == 1, "sliced compute covers the single-B case");
 #pragma unroll
     for (int u = u0; u < u1; ++u) {
       const int kk = u / TN, jn = u % TN;
@@ -460,23 +455,26 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
             af_s[p][i] = *reinterpret_cast<const bf16x8*>(
                 As + ((buf * NA + p) * BM + wm * WM + i * 32 + (lane & 31)) * LDK + kof);
       }
-      bf16x8 bfr;
-      if constexpr (BT) {
-        const int g4 = lane >> 4, s16 = lane & 15;
-        const int nb = wn * WN + jn * 32 + 16 * (g4 & 1);
-        const int kr0 = kk * 16 + 8 * (g4 >> 1) + (s16 >> 2);
-        const bf16* bp = Bs + (buf * BK + kr0) * PB + nb + 4 * (s16 & 3);
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp + 4 * PB));
-        bfr = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      } else {
-        bfr = *reinterpret_cast<const bf16x8*>(Bs + (buf * BN + wn * WN + jn * 32 + (lane & 31)) * LDK + kof);
+#pragma unroll
+      for (int q = 0; q < NB; ++q) {
+        bf16x8 bfr;
+        if constexpr (BT) {
+          const int g4 = lane >> 4, s16 = lane & 15;
+          const int nb = wn * WN + jn * 32 + 16 * (g4 & 1);
+          const int kr0 = kk * 16 + 8 * (g4 >> 1) + (s16 >> 2);
+          const bf16* bp = Bs + ((buf * NB + q) * BK + kr0) * PB + nb + 4 * (s16 & 3);
+          const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp));
+          const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp + 4 * PB));
+          bfr = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        } else {
+          bfr = *reinterpret_cast<const bf16x8*>(Bs + ((buf * NB + q) * BN + wn * WN + jn * 32 + (lane & 31)) * LDK + kof);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int p = 0; p < NA; ++p)
+            acc[q][i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af_s[p][i], bfr, acc[q][i][jn], 0, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int p = 0; p < NA; ++p)
-          acc[0][i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af_s[p][i], bfr, acc[0][i][jn], 0, 0, 0);
     }
   };
 
