@@ -32,12 +32,14 @@
 // and B in one L2.
 //
 // hw variant 1 keeps PD register sets of global loads in flight (PD = 3 for
-// tiles up to 128 x 128, 2 above) and stages B as loaded, [k][n], so every
-// B load instruction reads whole 128-byte lines (variant 0's transposing
-// register staging reads half lines, and a CU's vector L1 delivers about
-// half the useful bytes per cycle on half lines). The MFMA B fragments then
-// come from gfx950's transposing LDS read (ds_read_b64_tr_b16): two reads
-// give a lane the 8 consecutive k values of its column.
+// tiles up to 128 x 128, 2 above) in the plain order (all stores, refill,
+// then the MFMAs). Both variants stage B as loaded, [k][n], so every B load
+// instruction reads whole 128-byte lines (staging B transposed through
+// registers reads half lines, and a CU's vector L1 delivers about half the
+// useful bytes per cycle on half lines). The MFMA B fragments then come from
+// gfx950's transposing LDS read (ds_read_b64_tr_b16): two reads give a lane
+// the 8 consecutive k values of its column. (The register-transposed B path
+// below is kept for instantiations outside both variants.)
 //
 // Tile arguments: TILES_IN_BLOCK_M = BM/64, TILES_IN_BLOCK_N = BN/64 (tiles of
 //                 64, 128 or 256), TILES_IN_BLOCK_K = K range per workgroup /
@@ -66,7 +68,7 @@ constexpr int BK = 64;
 constexpr int kKUnit = 256;  // TILES_IN_BLOCK_K counts K in units of 256
 constexpr int LDK = BK + 8;  // LDS row pitch in elements (144 B; keeps 16 B alignment)
 
-// Row pitch (elements) of the [k][n] B tile of hw variant 1: BN + 16 puts the
+// Row pitch (elements) of the [k][n] B tile: BN + 16 puts the
 // four k rows one transposing read touches 8 banks apart.
 constexpr int bpitch(int BN) { return BN + 16; }
 constexpr int kThreads = 256;
@@ -117,12 +119,9 @@ template <int N>
 using ic = std::integral_constant<int, N>;
 
 // Prefetch depth 1 (hw variant 0, every epilogue) runs the rolling refill
-// with sliced compute (gemm_kernel's step); its B is staged as loaded and
-// read with the transposing LDS read, like every deeper pipeline.
-template <int EPI, int PD, bool AF>
+// with sliced compute (gemm_kernel's step).
+template <int PD>
 constexpr bool rolling() { return PD == 1; }
-template <int EPI, int PD, bool AF>
-constexpr bool b_transposed() { return PD > 1 || rolling<EPI, PD, AF>(); }
 
 template <int BM, int BN, int EPI, bool A_F32, int PD>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
@@ -136,11 +135,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   static_assert(AV >= 1 && KR >= 2 && KR <= 8, "tile shape");
 
   extern __shared__ __align__(16) unsigned char smem[];
-  // B is staged transposed ([n][k], pitch LDK) with one register set (hw
-  // variant 0), or as loaded ([k][n], pitch PB) and read with the
-  // transposing LDS read (several register sets, hw variant 1).
-  constexpr bool BT = b_transposed<EPI, PD, A_F32>();
-  constexpr bool ROLL = rolling<EPI, PD, A_F32>();
+  // B is staged as loaded ([k][n], pitch PB) and read with the transposing
+  // LDS read.
+  constexpr bool ROLL = rolling<PD>();
   constexpr int PB = bpitch(BN);
   bf16* As = reinterpret_cast<bf16*>(smem);                 // [2][NA][BM][LDK]
   bf16* Bs = As + 2 * NA * BM * LDK;                        // [2][NB][BN][LDK] or [2][NB][BK][PB]
@@ -171,13 +168,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 
   // Global-load assignment.
   // A: vector v = tid + j*256 -> row v/8, k-chunk v%8.
-  // B: thread -> (k block kb, column chunk nc): rows kb*KR..+KR, columns nc*8..+8.
-  // kb varies fastest across lanes: the transposed LDS stores of one
-  // instruction then fill contiguous KR-element runs of the same rows (no
-  // bank conflicts), at the price of less coalesced global loads.
-  constexpr int KBN = BK / KR;
-  const int b_kb = tid % KBN;
-  const int b_nc = tid / KBN;
+  // B: vector v = tid + r*256 -> k row v / (BN/8), column chunk v % (BN/8):
+  // whole 128-byte lines per instruction.
 
   // Global loads are unconditional from clamped (always in-range)
   // addresses, so the compiler issues them back to back and only waits for
@@ -229,12 +221,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     const int kl = min(k0, klast);
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
-      // Variant 0: rows b_kb*KR + r of column chunk b_nc. Variant 1: vector
-      // v = tid + r*256 -> row v / (BN/8), chunk v % (BN/8): whole 128-byte
-      // lines per instruction.
       const int v = tid + r * kThreads;
-      const int kr = BT ? v / (BN / 8) : b_kb * KR + r;
-      const int gn = n0 + (BT ? v % (BN / 8) : b_nc) * 8;
+      const int kr = v / (BN / 8);
+      const int gn = n0 + (v % (BN / 8)) * 8;
       const int gk = k0 + kr;
       b_ok[P][r] = gk < kend && gn < g.N;
       const int64_t off = static_cast<int64_t>(min(kl + kr, g.K - 1)) * ldbc + min(gn - ncol0, ldbc - 8);
@@ -324,59 +313,18 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     constexpr int P = decltype(set_tag)::value;
     auto& b_raw_p = b_raw[P];
     auto& b_ok_p = b_ok[P];
-    if constexpr (BT) {
 #pragma unroll
-      for (int q = 0; q < NB; ++q)
-#pragma unroll
-        for (int r = 0; r < KR; ++r) {
-          // Opaque until here: otherwise the zeroing below is placed right
-          // after the load and waits for it PD steps early.
-          u32x4 raw = *reinterpret_cast<const u32x4*>(&b_raw_p[q][r]);
-          asm volatile("" : "+v"(raw));
-          if (!b_ok_p[r]) raw = u32x4{0u, 0u, 0u, 0u};
-          const int v = tid + r * kThreads;
-          *reinterpret_cast<u32x4*>(Bs + ((buf * NB + q) * BK + v / (BN / 8)) * PB + (v % (BN / 8)) * 8) = raw;
-        }
-      return;
-    }
-#pragma unroll
-    for (int q = 0; q < NB; ++q) {
-      bf16 bv[KR][8];
+    for (int q = 0; q < NB; ++q)
 #pragma unroll
       for (int r = 0; r < KR; ++r) {
-        // Opaque until here: otherwise the 16-bit extractions below are
-        // placed right after the load and wait for it PD steps early.
+        // Opaque until here: otherwise the zeroing below is placed right
+        // after the load and waits for it PD steps early.
         u32x4 raw = *reinterpret_cast<const u32x4*>(&b_raw_p[q][r]);
-        if constexpr (PD > 1) asm volatile("" : "+v"(raw));
-        Vec<bf16> t;
-        *reinterpret_cast<u32x4*>(&t) = raw;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bv[r][e] = b_ok_p[r] ? t.v[e] : static_cast<bf16>(0.f);
+        asm volatile("" : "+v"(raw));
+        if (!b_ok_p[r]) raw = u32x4{0u, 0u, 0u, 0u};
+        const int v = tid + r * kThreads;
+        *reinterpret_cast<u32x4*>(Bs + ((buf * NB + q) * BK + v / (BN / 8)) * PB + (v % (BN / 8)) * 8) = raw;
       }
-      bf16* dst = Bs + ((buf * NB + q) * BN + b_nc * 8) * LDK + b_kb * KR;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        // KR k-values of column b_nc*8 + i.
-        if constexpr (KR == 8) {
-          Vec<bf16> t;
-#pragma unroll
-          for (int r = 0; r < 8; ++r) t.v[r] = bv[r][i];
-          store_vec(dst + i * LDK, t);
-        } else if constexpr (KR == 4) {
-          typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-          bf16x4 t;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) t[r] = bv[r][i];
-          *reinterpret_cast<bf16x4*>(dst + i * LDK) = t;
-        } else {
-          typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-          bf16x2 t;
-          t[0] = bv[0][i];
-          t[1] = bv[1][i];
-          *reinterpret_cast<bf16x2*>(dst + i * LDK) = t;
-        }
-      }
-    }
   };
   auto store_lds = [&](int buf, auto set_tag) {
 #pragma unroll
@@ -409,24 +357,18 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
       for (int q = 0; q < NB; ++q) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          bf16x8 bfr;
-          if constexpr (BT) {
-            // Transposing read: within each 16-lane group, lane i receives
-            // element i%4 of the 4 values lane 4j + i/4 points at, for j =
-            // 0..3. Lane s points at row k0 + s/4, columns nb + 4*(s%4), so
-            // lane i gets k rows k0..k0+3 of column nb + i; a second read
-            // 4 rows down gives k0+4..k0+7 (the MFMA's 8 k values).
-            const int g4 = lane >> 4, s16 = lane & 15;
-            const int nb = wn * WN + j * 32 + 16 * (g4 & 1);
-            const int kr0 = kk * 16 + 8 * (g4 >> 1) + (s16 >> 2);
-            const bf16* bp = Bs + ((buf * NB + q) * BK + kr0) * PB + nb + 4 * (s16 & 3);
-            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp));
-            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp + 4 * PB));
-            bfr = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          } else {
-            bfr = *reinterpret_cast<const bf16x8*>(
-                Bs + ((buf * NB + q) * BN + wn * WN + j * 32 + (lane & 31)) * LDK + kof);
-          }
+          // Transposing read: within each 16-lane group, lane i receives
+          // element i%4 of the 4 values lane 4j + i/4 points at, for j =
+          // 0..3. Lane s points at row k0 + s/4, columns nb + 4*(s%4), so
+          // lane i gets k rows k0..k0+3 of column nb + i; a second read
+          // 4 rows down gives k0+4..k0+7 (the MFMA's 8 k values).
+          const int g4 = lane >> 4, s16 = lane & 15;
+          const int nb = wn * WN + j * 32 + 16 * (g4 & 1);
+          const int kr0 = kk * 16 + 8 * (g4 >> 1) + (s16 >> 2);
+          const bf16* bp = Bs + ((buf * NB + q) * BK + kr0) * PB + nb + 4 * (s16 & 3);
+          const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp));
+          const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp + 4 * PB));
+          const bf16x8 bfr = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
           for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -457,18 +399,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
       }
 #pragma unroll
       for (int q = 0; q < NB; ++q) {
-        bf16x8 bfr;
-        if constexpr (BT) {
-          const int g4 = lane >> 4, s16 = lane & 15;
-          const int nb = wn * WN + jn * 32 + 16 * (g4 & 1);
-          const int kr0 = kk * 16 + 8 * (g4 >> 1) + (s16 >> 2);
-          const bf16* bp = Bs + ((buf * NB + q) * BK + kr0) * PB + nb + 4 * (s16 & 3);
-          const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp));
-          const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp + 4 * PB));
-          bfr = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        } else {
-          bfr = *reinterpret_cast<const bf16x8*>(Bs + ((buf * NB + q) * BN + wn * WN + jn * 32 + (lane & 31)) * LDK + kof);
-        }
+        const int g4 = lane >> 4, s16 = lane & 15;
+        const int nb = wn * WN + jn * 32 + 16 * (g4 & 1);
+        const int kr0 = kk * 16 + 8 * (g4 >> 1) + (s16 >> 2);
+        const bf16* bp = Bs + ((buf * NB + q) * BK + kr0) * PB + nb + 4 * (s16 & 3);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bp + 4 * PB));
+        const bf16x8 bfr = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -1138,8 +1075,8 @@ bool tile_ok(int tm, int tn) {
   return (tm == 1 || tm == 2 || tm == 4) && (tn == 1 || tn == 2 || tn == 4);
 }
 
-size_t lds_bytes(int BM, int BN, int na, int nb, bool btile = false) {
-  const size_t b = btile ? static_cast<size_t>(BK) * bpitch(BN) : static_cast<size_t>(BN) * LDK;
+size_t lds_bytes(int BM, int BN, int na, int nb) {
+  const size_t b = static_cast<size_t>(BK) * bpitch(BN);
   return static_cast<size_t>(2) * (na * BM * LDK + nb * b) * sizeof(bf16);
 }
 
@@ -1197,7 +1134,7 @@ size_t gemm_workspace(int M, int N, int K, int tm, int tn, int tk, int nb) {
 template <int BM, int BN, int EPI, bool AF, int PD>
 void launch_tile(const GemmArgs& g, hipStream_t st) {
   constexpr int na = AF ? 2 : 1, nb = EPI == kSiluMul ? 2 : 1;
-  const size_t lds = lds_bytes(BM, BN, na, nb, b_transposed<EPI, PD, AF>());
+  const size_t lds = lds_bytes(BM, BN, na, nb);
   auto fn = gemm_kernel<BM, BN, EPI, AF, PD>;
   // Raising the dynamic LDS limit is idempotent, so a race between threads
   // doing it for the first time is harmless.
