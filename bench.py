@@ -11,20 +11,31 @@ FLOPs).
 
 Timing: inputs are resident in HBM before the timed region. Launches rotate
 over enough copies of the input/output set to exceed 1 GiB, so the 256 MB
-Infinity Cache cannot serve a set that was just touched. `--warmup` untimed
-launches, then exactly `--steps` launches between two HIP events recorded on
-the stream the kernels are launched on, bracketed by device syncs; the
-average launch duration is the elapsed time / steps. After an idle second
-(the CPU baseline legs leave the GPU idle) the clocks take about 30 ms of
-back-to-back launches to settle: the 33 us matmul runs its first launches
-at 240 us and its next 25 at 42 us, so the default warmup of 2000 launches
-keeps every workload's ramp out of the timed region.
+Infinity Cache cannot serve a set that was just touched. Before each
+workload's timed region the kernel runs untimed back-to-back launches until
+both `--warmup` launches and `--settle-ms` (default 50 ms) of device time
+are behind it: after an idle second (the CPU baseline legs leave the GPU
+idle) the clocks take about 30 ms of back-to-back launches to settle, and a
+launch count alone (the 33 us matmul runs its first launches at 240 us and
+its next 25 at 42 us) would time the ramp. The settle each workload got is
+reported (`settle_ms`, `settle_launches`). Then exactly `--steps` launches
+run between two HIP events recorded on the stream the kernels are launched
+on, bracketed by device syncs; the average launch duration is the elapsed
+time / steps.
+
+Correctness: after timing, each workload's outputs are filled with NaN, the
+kernel is launched once more, and the result is compared with the oracle
+restatement of the spec's torch reference (fp32 on the host) at that
+workload's tolerance (rtol = atol = 1e-2 for bf16 outputs; rtol 1e-5,
+atol 0 for the fp32 scan of probabilities). Every row carries `allclose`
+and `max_abs_err`; the process exits 1 after printing the JSON line if any
+row misses.
 
 CPU baseline: the oracle restatement of the same math, timed on the host
-cores (torch, all affinity cores) on the full headline shape; its output is
-also compared with the GPU output as a last guard.
+cores (torch, all affinity cores) on the full shape of each workload.
 
-Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 2000] [--headline-only]
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--settle-ms 50]
+       [--headline-only] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -50,49 +61,57 @@ ROTATE_BYTES = 1 << 30
 METRIC = "achieved HBM GB/s (% peak) per norm/rope/scan; MFMA TFLOP/s for matmul/attn"
 
 # name, sizes, variant, tiles (picked by the tile sweep on MI355X), bound,
-# algorithmic work per launch (bytes for "hbm", FLOPs for "mfma"), label.
-# The bound is the larger of the two lower limits, bytes / 8 TB/s and
-# FLOPs / 2.5 PFLOP/s: qkv_cte's three [16384,8192] residual inputs make it
-# HBM-bound (830 MB: 104 us) although it is a GEMM (137 GFLOP: 55 us); its
-# row also reports the MFMA rate (`flops`).
+# algorithmic work per launch (bytes for "hbm", FLOPs for "mfma"), the
+# correctness tolerance of the row, label. The bound is the larger of the two
+# lower limits, bytes / 8 TB/s and FLOPs / 2.5 PFLOP/s: qkv_cte's three
+# [16384,8192] residual inputs make it HBM-bound (830 MB: 104 us) although it
+# is a GEMM (137 GFLOP: 55 us); its row also reports the MFMA rate (`flops`).
+# Tolerances: bf16 outputs rtol = atol = 1e-2; the fp32 scan of probabilities
+# rtol 1e-5, atol 0; qkv_cte (bf16, outputs ~N(0,1) after a 8192-deep
+# product) rtol = atol = 2e-2, tighter than its own case tolerance (5e-2 /
+# 1.5e-1 in eval/sizes.json).
 CONFIGS = [
     dict(
         spec="rope_llama3", sizes=(1, 4096, 32, 8, 128), variant=0, tiles=(4, 1), bound="hbm",
-        work=88_080_384,
+        work=88_080_384, rtol=1e-2, atol=1e-2,
         label="RoPE Llama-3-8B: q[1,4096,32,128] k[1,4096,8,128] bf16, cos/sin[4096,128] fp32, theta 500000",
     ),
     dict(
         spec="rmsnorm_weighted", sizes=(2048, 4096), variant=0, tiles=(2, 2), bound="hbm",
-        work=33_562_624,
+        work=33_562_624, rtol=1e-2, atol=1e-2,
         label="RMSNorm x[2048,4096] bf16, weight[4096] bf16, eps 1e-6",
     ),
     dict(
         spec="cumsum_probs", sizes=(64, 128256), variant=2, tiles=(8, 4), bound="hbm",
-        work=65_667_072,
+        work=65_667_072, rtol=1e-5, atol=0.0,
         label="cumsum over vocab: probs[64,128256] fp32 (sorted softmax of N(0,3) logits)",
     ),
     dict(
         spec="matmul_std002", sizes=(1024, 512, 16384), variant=1, tiles=(2, 2, 8), bound="mfma",
-        work=2 * 1024 * 512 * 16384,
+        work=2 * 1024 * 512 * 16384, rtol=1e-2, atol=1e-2,
         label="matmul m,n,k = 1024,512,16384 bf16 N(0,0.02), fp32 accumulate",
     ),
     dict(
         spec="rmsnorm_matmul_eps", sizes=(1024, 512, 16384), variant=1, tiles=(2, 2, 8), bound="mfma",
-        work=2 * 1024 * 512 * 16384,
+        work=2 * 1024 * 512 * 16384, rtol=1e-2, atol=1e-2,
         label="rmsnorm_matmul m,n,k = 1024,512,16384 bf16, eps 1e-6",
     ),
     dict(
         spec="attention_causal", sizes=(1, 32, 4096, 128), variant=2, tiles=(2, 2, 1, 1), bound="mfma",
-        work=137_438_953_472,
+        work=137_438_953_472, rtol=1e-2, atol=1e-2,
         label="causal attention Q/K/V [1,32,4096,128] bf16, scale 1/sqrt(128)",
     ),
     dict(
         spec="qkv_cte", sizes=(16384, 512, 8192), variant=2, tiles=(4, 4, 16), bound="hbm",
         work=3 * 16384 * 8192 * 2 + 8192 * 512 * 2 + 16384 * 512 * 2, flops=2 * 16384 * 512 * 8192,
+        rtol=2e-2, atol=2e-2,
         label="qkv_cte llama70b: x, mlp_prev, attention_prev [16384,8192] bf16 summed, RMSNorm eps 1e-6, "
               "@ w [8192,512] bf16",
     ),
 ]
+
+SETTLE_MS = 50.0
+MAX_SETTLE_LAUNCHES = 200_000
 
 
 def load_spec(name: str):
@@ -101,9 +120,49 @@ def load_spec(name: str):
     return _load_spec(str(REPO / "kernels" / name))
 
 
-def measure(cfg: dict, steps: int, warmup: int):
-    """Average launch duration (us) over `steps` back-to-back launches that
-    rotate over >= 1 GiB of buffer sets; returns (avg_us, first outputs, host inputs)."""
+def timed_launches(launch, n_sets: int, steps: int, warmup: int, settle_ms: float, stream):
+    """Settle the clocks, then time `steps` back-to-back launches.
+
+    `launch(i)` enqueues one launch on buffer set i on `stream`. Untimed
+    launches run first until at least `warmup` of them and `settle_ms` of
+    device time (HIP events on `stream`) are behind; the chunks double so the
+    last one covers at least half the settle period without host gaps.
+    Returns (average us per timed launch, settle ms, settle launches)."""
+    import torch
+
+    w0 = torch.cuda.Event(enable_timing=True)
+    w1 = torch.cuda.Event(enable_timing=True)
+    w0.record(stream)
+    done = 0
+    for _ in range(max(0, warmup)):
+        launch(done % n_sets)
+        done += 1
+    w1.record(stream)
+    torch.cuda.synchronize()
+    chunk = max(1, done)
+    while w0.elapsed_time(w1) < settle_ms and done < MAX_SETTLE_LAUNCHES:
+        for _ in range(chunk):
+            launch(done % n_sets)
+            done += 1
+        w1.record(stream)
+        torch.cuda.synchronize()
+        chunk *= 2
+    settled = w0.elapsed_time(w1)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        launch((done + i) % n_sets)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / steps, settled, done
+
+
+def measure(cfg: dict, steps: int, warmup: int, settle_ms: float):
+    """Times `cfg` (see timed_launches) over buffer sets rotating through
+    >= 1 GiB, then launches once more on NaN-filled outputs and returns
+    (avg_us, settle_ms, settle_launches, fresh outputs on the host as fp32,
+    host inputs)."""
     import torch
 
     from enzyme_amd import hip
@@ -124,22 +183,19 @@ def measure(cfg: dict, steps: int, warmup: int):
         for _ in range(n_sets - 1)
     ]
     stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        sets[i % n_sets].launch(stream)
+    avg_us, settled, launches = timed_launches(
+        lambda i: sets[i].launch(stream), n_sets, steps, warmup, settle_ms, stream)
+    for o in first.outputs:
+        o.fill_(float("nan"))
+    first.launch(stream)
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(steps):
-        sets[i % n_sets].launch(stream)
-    end.record(stream)
-    torch.cuda.synchronize()
-    avg_us = start.elapsed_time(end) * 1e3 / steps
     outs = [o.float().cpu() for o in first.outputs]
-    return avg_us, outs, host, spec
+    del sets, first, dev
+    torch.cuda.empty_cache()
+    return avg_us, settled, launches, outs, host
 
 
-def measure_copy(nbytes: int, steps: int, warmup: int) -> float:
+def measure_copy(nbytes: int, steps: int, warmup: int, settle_ms: float) -> float:
     """Average duration (us) of a plain 16-byte-vector device copy that reads
     and writes `nbytes` each, rotating over >= 1 GiB of buffer pairs: the
     practical HBM ceiling for a kernel moving 2 * nbytes."""
@@ -152,22 +208,39 @@ def measure_copy(nbytes: int, steps: int, warmup: int) -> float:
     sets = [(torch.empty(nbytes, dtype=torch.uint8, device="cuda"),
              torch.empty(nbytes, dtype=torch.uint8, device="cuda")) for _ in range(n_sets)]
     stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        hip.copy(*sets[i % n_sets])
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(steps):
-        hip.copy(*sets[i % n_sets])
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) * 1e3 / steps
+    us, _, _ = timed_launches(lambda i: hip.copy(*sets[i]), n_sets, steps, warmup, settle_ms, stream)
+    del sets
+    torch.cuda.empty_cache()
+    return us
 
 
-def cpu_baseline(cfg: dict, host, gpu_outs, runs: int = 10):
-    """The oracle on the host cores: (median seconds, threads, max error of
-    the GPU output against it)."""
+def oracle_outputs(cfg: dict, host):
+    """fp32 oracle outputs (tuple) of the spec's torch reference on the host."""
+    import torch
+
+    import oracle
+    from enzyme_amd.dtypes import to_f32_torch
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    with torch.no_grad():
+        ref = oracle.ORACLE[cfg["spec"]](*[to_f32_torch(a) for a in host])
+    return ref if isinstance(ref, tuple) else (ref,)
+
+
+def verdict(cfg: dict, gpu_outs, refs) -> dict:
+    """allclose of every GPU output against the oracle at the row's tolerance."""
+    import torch
+
+    ok = all(
+        bool(torch.isfinite(g).all()) and torch.allclose(g, r, rtol=cfg["rtol"], atol=cfg["atol"])
+        for g, r in zip(gpu_outs, refs)
+    )
+    err = max(float((g - r).abs().max()) for g, r in zip(gpu_outs, refs))
+    return {"allclose": ok, "rtol": cfg["rtol"], "atol": cfg["atol"], "max_abs_err": err}
+
+
+def cpu_baseline(cfg: dict, host, runs: int = 10):
+    """The oracle on the host cores: (median seconds, threads)."""
     import torch
 
     import oracle
@@ -179,16 +252,13 @@ def cpu_baseline(cfg: dict, host, gpu_outs, runs: int = 10):
     args = [to_f32_torch(a) for a in host]
     with torch.no_grad():
         for _ in range(2):
-            ref = fn(*args)
+            fn(*args)
         times = []
         for _ in range(runs):
             t0 = time.perf_counter()
-            ref = fn(*args)
+            fn(*args)
             times.append(time.perf_counter() - t0)
-    refs = ref if isinstance(ref, tuple) else (ref,)
-    err = max(float((g - r).abs().max()) for g, r in zip(gpu_outs, refs))
-    ok = all(torch.allclose(g, r, rtol=1e-2, atol=1e-2) for g, r in zip(gpu_outs, refs))
-    return float(np.median(times)), torch.get_num_threads(), err, ok
+    return float(np.median(times)), torch.get_num_threads()
 
 
 def roofline(cfg: dict, avg_us: float) -> dict:
@@ -218,9 +288,11 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="minimum device time of untimed launches before each timed region")
     ap.add_argument("--headline-only", action="store_true")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline timing")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(
@@ -235,16 +307,42 @@ def main(argv=None) -> int:
         print("bench.py needs a visible GPU", file=sys.stderr)
         return 2
 
-    head = CONFIGS[0]
-    avg_us, outs, host, _ = measure(head, args.steps, args.warmup)
+    rows = []
+    for cfg in CONFIGS[:1] if args.headline_only else CONFIGS:
+        us, settled, launches, outs, host = measure(cfg, args.steps, args.warmup, args.settle_ms)
+        row = {"spec": cfg["spec"], "label": cfg["label"], "sizes": list(cfg["sizes"]),
+               "tiles": list(cfg["tiles"]), "hw_variant": cfg["variant"], "us_per_launch": round(us, 3),
+               "settle_ms": round(settled, 2), "settle_launches": launches,
+               **roofline(cfg, us), "traffic": traffic_for(cfg["spec"])}
+        if "flops" in cfg:
+            tf = cfg["flops"] / (us * 1e-6) / 1e12
+            row["mfma"] = {"achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+        if cfg["bound"] == "hbm":
+            cu = measure_copy(cfg["work"] // 2, args.steps, args.warmup, args.settle_ms)
+            row["copy_us"] = round(cu, 3)
+            row["vs_copy"] = round(cu / us, 4)
+        row.update(verdict(cfg, outs, oracle_outputs(cfg, host)))
+        if not args.no_cpu:
+            runs = 3 if cfg["spec"] in ("attention_causal", "qkv_cte") else 10
+            sec, threads = cpu_baseline(cfg, host, runs=runs)
+            row["cpu_ms"] = round(sec * 1e3, 3)
+            row["cpu_cores"] = threads
+        rows.append(row)
+        print(f"# {cfg['spec']}: {us:.2f} us, {row['achieved']} {row['unit']} "
+              f"({100 * row['frac']:.1f}% of peak), allclose {row['allclose']} "
+              f"(max abs err {row['max_abs_err']:.3g}), settle {settled:.1f} ms / {launches} launches",
+              file=sys.stderr, flush=True)
+
+    head, hrow = CONFIGS[0], rows[0]
     line = {
         "metric": METRIC,
-        "value": None,
-        "unit": "GB/s",
+        "value": hrow["achieved"],
+        "unit": hrow["unit"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(avg_us / 1e3, 6),
+        "ms_per_step": round(hrow["us_per_launch"] / 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -257,59 +355,35 @@ def main(argv=None) -> int:
             "hw_variant": head["variant"],
             "tiles": list(head["tiles"]),
         },
-    }
-    rf = roofline(head, avg_us)
-    rf["traffic"] = traffic_for(head["spec"])
-    line["value"] = rf["achieved"]
-    line["roofline"] = rf
-    copy_us = measure_copy(head["work"] // 2, args.steps, args.warmup)
-    line["copy_ceiling"] = {
-        "us": round(copy_us, 3),
-        "achieved": round(head["work"] / (copy_us * 1e-6) / 1e9, 2),
-        "unit": "GB/s",
-        "what": "plain 16-byte-vector copy reading and writing half the headline's algorithmic "
-                "bytes each, same buffer rotation: the HBM rate a streaming kernel of this size "
-                "reaches here",
-    }
-    if not args.no_cpu:
-        sec, threads, err, ok = cpu_baseline(head, host, outs)
-        line["cpu_baseline"] = {
-            "value": round(head["work"] / sec / 1e9, 3),
+        "settle_ms": hrow["settle_ms"],
+        "settle_launches": hrow["settle_launches"],
+        "allclose": hrow["allclose"],
+        "roofline": {k: hrow[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+        "copy_ceiling": {
+            "us": hrow["copy_us"],
+            "achieved": round(head["work"] / (hrow["copy_us"] * 1e-6) / 1e9, 2),
             "unit": "GB/s",
-            "cores": threads,
+            "what": "plain 16-byte-vector copy reading and writing half the headline's algorithmic "
+                    "bytes each, same buffer rotation: the HBM rate a streaming kernel of this size "
+                    "reaches here",
+        },
+    }
+    if "cpu_ms" in hrow:
+        line["cpu_baseline"] = {
+            "value": round(head["work"] / (hrow["cpu_ms"] * 1e-3) / 1e9, 3),
+            "unit": "GB/s",
+            "cores": hrow["cpu_cores"],
             "kind": "port",
             "sample": "oracle (fp32 torch restatement of the spec's torch_ref) on the full headline "
-                      f"shape, median of 10 runs after 2 warmups: {sec * 1e3:.2f} ms per pass",
-            "gpu_max_abs_err": err,
-            "gpu_allclose_1e-2": ok,
+                      f"shape, median of 10 runs after 2 warmups: {hrow['cpu_ms']:.2f} ms per pass",
         }
     if not args.headline_only:
-        rows = []
-        for cfg in CONFIGS:
-            steps = args.steps
-            us, o, h, _ = measure(cfg, steps, args.warmup)
-            row = {"spec": cfg["spec"], "label": cfg["label"], "tiles": list(cfg["tiles"]),
-                   "hw_variant": cfg["variant"], "us_per_launch": round(us, 3), **roofline(cfg, us),
-                   "traffic": traffic_for(cfg["spec"])}
-            if "flops" in cfg:
-                tf = cfg["flops"] / (us * 1e-6) / 1e12
-                row["mfma"] = {"achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                               "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
-            if cfg["bound"] == "hbm":
-                cu = measure_copy(cfg["work"] // 2, steps, args.warmup)
-                row["copy_us"] = round(cu, 3)
-                row["vs_copy"] = round(cu / us, 4)
-            if not args.no_cpu:
-                runs = 3 if cfg["spec"] in ("attention_causal", "qkv_cte") else 10
-                sec, threads, err, ok = cpu_baseline(cfg, h, o, runs=runs)
-                row["cpu_ms"] = round(sec * 1e3, 3)
-                row["cpu_cores"] = threads
-                row["gpu_max_abs_err"] = err
-            rows.append(row)
-            print(f"# {cfg['spec']}: {us:.2f} us, {row['achieved']} {row['unit']} "
-                  f"({100 * row['frac']:.1f}% of peak)", file=sys.stderr, flush=True)
         line["configs"] = rows
     print(json.dumps(line))
+    failed = [r["spec"] for r in rows if not r["allclose"]]
+    if failed:
+        print(f"bench.py: outputs outside tolerance for {', '.join(failed)}", file=sys.stderr)
+        return 1
     return 0
 
 

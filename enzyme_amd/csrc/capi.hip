@@ -306,4 +306,6 @@ int axon_copy(const void* src, void* dst, size_t bytes, axon_stream_t stream) {
   return launch_status("copy_kernel");
 }
 
+uint32_t axon_scan_poll_bound(uint32_t polls) { return axon::set_scan_poll_bound(polls); }
+
 }  // extern "C"

@@ -38,8 +38,7 @@
 // registers reads half lines, and a CU's vector L1 delivers about half the
 // useful bytes per cycle on half lines). The MFMA B fragments then come from
 // gfx950's transposing LDS read (ds_read_b64_tr_b16): two reads give a lane
-// the 8 consecutive k values of its column. (The register-transposed B path
-// below is kept for instantiations outside both variants.)
+// the 8 consecutive k values of its column.
 //
 // Tile arguments: TILES_IN_BLOCK_M = BM/64, TILES_IN_BLOCK_N = BN/64 (tiles of
 //                 64, 128 or 256), TILES_IN_BLOCK_K = K range per workgroup /
@@ -140,7 +139,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   constexpr bool ROLL = rolling<PD>();
   constexpr int PB = bpitch(BN);
   bf16* As = reinterpret_cast<bf16*>(smem);                 // [2][NA][BM][LDK]
-  bf16* Bs = As + 2 * NA * BM * LDK;                        // [2][NB][BN][LDK] or [2][NB][BK][PB]
+  bf16* Bs = As + 2 * NA * BM * LDK;                        // [2][NB][BK][PB]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1735,7 +1734,7 @@ const char* summary_softmax_mm(int variant) {
 }
 
 // ---- linear_attention (dims sq, sk, dk, dv; q [sq,dk], key [sk,dk], v [sk,dv])
-// out = q (keyᵀ v) (kernels/linear_attention/kernel.py:16-27): key is
+// out = q (keyᵀ v) (kernels/linear_attention/kernel.py:14-20): key is
 // transposed into the workspace, state = keyᵀ v is a split-K GEMM over sk
 // (bf16 state, fp32 accumulation), then out = q state over dk.
 // Tiles: TILES_IN_BLOCK_P = state rows per tile / 64 (over dk),

@@ -82,4 +82,8 @@ inline const char* dtype_str(int d) {
 
 inline int elem_bytes(int d) { return d == AXON_F32 ? 4 : 2; }
 
+// Poll bound of the single-pass cumsum variant (scan.hip); returns the
+// previous bound.
+unsigned set_scan_poll_bound(unsigned polls);
+
 }  // namespace axon

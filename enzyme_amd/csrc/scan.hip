@@ -29,10 +29,15 @@
 //   totals of the earlier chunks of its row as they appear (one poll round
 //   per lane in the common case). The tag is unique per launch (a counter in
 //   the library), so words left by earlier launches never match and the
-//   workspace needs no reset. Workgroups are dispatched in index order on
-//   each XCD, so a workgroup only waits for workgroups that are running or
-//   done; the polls are bounded anyway (an exhausted bound sets the error
-//   word in the workspace header and the kernel still finishes).
+//   workspace needs no reset. Correctness never depends on the order in
+//   which workgroups are dispatched: a lane polls an earlier chunk's word at
+//   most `max_polls` times, and a total that has not appeared by then is
+//   recomputed by the waiting wave from the input itself, in the publisher's
+//   own summation order, so it equals the published value bit for bit. The
+//   wait is then bounded by max_polls sleeps plus one chunk read per missing
+//   total, and every workgroup finishes. The workspace header's word 0
+//   counts the totals recomputed since the workspace was zeroed (a
+//   diagnostic; nothing reads it to decide a result).
 // Tile arguments: TILES_IN_BLOCK_M = W (waves per workgroup),
 //                 TILES_IN_BLOCK_N = V (16-byte vectors per lane per chunk).
 #include <atomic>
@@ -212,15 +217,45 @@ __global__ __launch_bounds__(1024) void chunk_scan_kernel(const T* __restrict__ 
   scan_store_chunk<T, V, ALIGNED>(v, y + row * n, c0, n, carry, wave_tot);
 }
 
-// Single-pass workspace: a header (word 0: poll-bound error flag) padded to
-// 256 bytes, then one 64-bit slot per chunk (row-major).
+// Single-pass workspace: a header (word 0: count of recomputed chunk totals)
+// padded to 256 bytes, then one 64-bit slot per chunk (row-major).
 constexpr size_t kOnepassHeader = 256;
-constexpr unsigned kMaxPolls = 1u << 16;
+
+// fp32 sum of one thread's V x E elements, in the order every total of the
+// single-pass variant uses (v outer, e inner).
+template <int V, int E>
+__device__ __forceinline__ float thread_total(const float (&x)[V][E]) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+#pragma unroll
+    for (int e = 0; e < E; ++e) s += x[i][e];
+  return s;
+}
+
+// The total of the chunk starting at c0, computed by one wave exactly as the
+// chunk's own workgroup computes it before publishing: per wave w of that
+// workgroup, the double wave64 sum of its threads' fp32 totals, added in w
+// order in double. Same value on every lane.
+template <typename T, int V, bool ALIGNED>
+__device__ double recompute_chunk_total(const T* __restrict__ xr, int64_t c0, int64_t n, int nw,
+                                        int lane) {
+  constexpr int E = EPV<T>::value;
+  const int64_t per_wave = static_cast<int64_t>(kWave) * V * E;
+  double t = 0.0;
+  for (int w = 0; w < nw; ++w) {
+    float v[V][E];
+    load_striped<T, V, ALIGNED, false>(xr, c0 + w * per_wave, lane, n, v);
+    t += wave_sum(static_cast<double>(thread_total<V, E>(v)));
+  }
+  return t;
+}
 
 template <typename T, int V, bool ALIGNED>
 __global__ __launch_bounds__(1024) void scan_onepass_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                             unsigned* hdr, unsigned long long* slots,
-                                                            int64_t n, int nchunks, unsigned tag) {
+                                                            int64_t n, int nchunks, unsigned tag,
+                                                            unsigned max_polls) {
   constexpr int E = EPV<T>::value;
   __shared__ float wave_tot[kMaxW];
   __shared__ double part[kMaxW];
@@ -231,17 +266,14 @@ __global__ __launch_bounds__(1024) void scan_onepass_kernel(const T* __restrict_
   const int64_t row = b / static_cast<unsigned>(nchunks);
   const int c = static_cast<int>(b - row * nchunks);
   const int64_t per_wave = static_cast<int64_t>(kWave) * V * E;
-  const int64_t c0 = static_cast<int64_t>(c) * nw * per_wave;
+  const int64_t chunk = static_cast<int64_t>(nw) * per_wave;
+  const int64_t c0 = static_cast<int64_t>(c) * chunk;
+  const T* xr = x + row * n;
   float v[V][E];
-  load_striped<T, V, ALIGNED, true>(x + row * n, c0 + wave * per_wave, lane, n, v);
+  load_striped<T, V, ALIGNED, true>(xr, c0 + wave * per_wave, lane, n, v);
 
   // Publish this chunk's total (not needed by the last chunk of a row).
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < V; ++i)
-#pragma unroll
-    for (int e = 0; e < E; ++e) s += v[i][e];
-  const double d = wave_sum(static_cast<double>(s));
+  const double d = wave_sum(static_cast<double>(thread_total<V, E>(v)));
   if (lane == 0) part[wave] = d;
   __syncthreads();
   if (threadIdx.x == 0 && c + 1 < nchunks) {
@@ -252,23 +284,40 @@ __global__ __launch_bounds__(1024) void scan_onepass_kernel(const T* __restrict_
     __hip_atomic_store(&slots[b], word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  // Carry: the totals of chunks 0..c-1 of this row (wave 0, one chunk per lane).
+  // Carry: the totals of chunks 0..c-1 of this row (wave 0, one chunk per
+  // lane per round of 64).
   if (wave == 0) {
     double acc = 0.0;
     const int64_t rowbase = row * nchunks;
-    for (int i = lane; i < c; i += kWave) {
-      unsigned long long w = 0;
-      for (unsigned polls = 0;; ++polls) {
-        w = __hip_atomic_load(&slots[rowbase + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (static_cast<unsigned>(w >> 32) == tag) break;
-        if (polls == kMaxPolls) {
-          __hip_atomic_store(&hdr[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          w = 0;
-          break;
+    for (int base = 0; base < c; base += kWave) {
+      const int i = base + lane;
+      bool have = false;
+      float t = 0.f;
+      if (i < c) {
+        for (unsigned polls = 0; polls < max_polls; ++polls) {
+          const unsigned long long w =
+              __hip_atomic_load(&slots[rowbase + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (static_cast<unsigned>(w >> 32) == tag) {
+            t = __uint_as_float(static_cast<unsigned>(w));
+            have = true;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
         }
-        __builtin_amdgcn_s_sleep(2);
       }
-      acc += static_cast<double>(__uint_as_float(static_cast<unsigned>(w)));
+      // Totals that did not appear within the bound: the wave sums each of
+      // those chunks from x (bounded work, same value as the publisher's).
+      unsigned long long missing = __ballot(i < c && !have);
+      if (missing != 0ull && lane == 0)
+        __hip_atomic_fetch_add(&hdr[0], static_cast<unsigned>(__popcll(missing)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      while (missing != 0ull) {
+        const int f = __builtin_ctzll(missing);
+        missing &= missing - 1ull;
+        const double tot = recompute_chunk_total<T, V, ALIGNED>(xr, (base + f) * chunk, n, nw, lane);
+        if (lane == f) t = static_cast<float>(tot);
+      }
+      if (i < c) acc += static_cast<double>(t);
     }
     acc = wave_sum(acc);
     if (lane == 0) s_carry = acc;
@@ -286,6 +335,12 @@ unsigned next_scan_tag() {
   if (t == 0) t = g_scan_tag.fetch_add(1, std::memory_order_relaxed) + 1;
   return t;
 }
+
+// How many times a single-pass lane polls for an earlier chunk's total before
+// recomputing it (each poll is one L2 load and a short sleep; a total
+// normally appears within a few polls).
+constexpr unsigned kDefaultPolls = 1u << 12;
+std::atomic<unsigned> g_scan_polls{kDefaultPolls};
 
 // ---------------------------------------------------------------------------
 // host side
@@ -378,7 +433,8 @@ void (*cscan_fn(int V))(const T*, T*, const double*, int64_t, int) {
   AXON_SCAN_PICK(chunk_scan_kernel, T, A, V)
 }
 template <typename T, bool A>
-void (*onepass_fn(int V))(const T*, T*, unsigned*, unsigned long long*, int64_t, int, unsigned) {
+void (*onepass_fn(int V))(const T*, T*, unsigned*, unsigned long long*, int64_t, int, unsigned,
+                          unsigned) {
   AXON_SCAN_PICK(scan_onepass_kernel, T, A, V)
 }
 
@@ -398,7 +454,7 @@ int launch_scan_ta(const Call& c, const T* x, T* y, void* ws, hipStream_t st) {
     unsigned* hdr = static_cast<unsigned*>(ws);
     auto* slots = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + kOnepassHeader);
     hipLaunchKernelGGL((onepass_fn<T, A>(V)), dim3(nblocks), block, 0, st, x, y, hdr, slots, n,
-                       nchunks, next_scan_tag());
+                       nchunks, next_scan_tag(), g_scan_polls.load(std::memory_order_relaxed));
     return launch_status("scan_onepass_kernel");
   }
   double* totals = static_cast<double*>(ws);
@@ -428,7 +484,8 @@ int launch_scan(const Call& c, const void* const* in, void* const* out, void* ws
 const char* summary_scan(int variant) {
   if (variant == 2)
     return "single pass: each chunk publishes a {launch tag, fp32 total} word and adds the "
-           "published totals of its row's earlier chunks (double carry); 1 read + 1 write, one "
+           "published totals of its row's earlier chunks (double carry), recomputing from the "
+           "input any total that does not appear within the poll bound; 1 read + 1 write, one "
            "launch";
   return variant == 0
              ? "row-resident stream: one workgroup per row, striped coalesced chunks scanned in "
@@ -439,6 +496,10 @@ const char* summary_scan(int variant) {
 }
 
 }  // namespace
+
+unsigned set_scan_poll_bound(unsigned polls) {
+  return g_scan_polls.exchange(polls, std::memory_order_relaxed);
+}
 
 const Family* family_cumsum() {
   static const Family f = {"cumsum", 3, 1, 1, 2, kTileArgs, 2, summary_scan, manifest_scan,

@@ -1,7 +1,7 @@
 """Host-side dtype handling for spec inputs, without `ml_dtypes`.
 
 The reference's spec packages draw float64 numbers from numpy and convert them
-with `.astype(ml_dtypes.bfloat16)` (kernels/rmsnorm/refs.py:81-82). That
+with `.astype(ml_dtypes.bfloat16)` (kernels/rmsnorm/refs.py:33-34). That
 package is not part of this stack, so a bf16 host array is a CPU
 `torch.bfloat16` tensor here. The conversion keeps the same rounding chain as
 ml_dtypes' double constructor: float64 -> float32 (round to nearest even),

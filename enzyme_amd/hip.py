@@ -60,6 +60,7 @@ EXPORTED_SYMBOLS = (
     "axon_variant_workspace",
     "axon_variant_launch",
     "axon_copy",
+    "axon_scan_poll_bound",
 )
 
 
@@ -120,6 +121,7 @@ def _declare(lib: ctypes.CDLL) -> None:
             ctypes.c_int,
             [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
         ),
+        "axon_scan_poll_bound": (ctypes.c_uint32, [ctypes.c_uint32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -366,6 +368,12 @@ def run_variant(meta: dict[str, Any], inputs: Sequence[Any], tiles: Sequence[int
     )
     ln.launch()
     return ln.outputs[0] if len(ln.outputs) == 1 else tuple(ln.outputs)
+
+
+def scan_poll_bound(polls: int) -> int:
+    """Set the single-pass cumsum poll bound (0 = always recompute earlier
+    chunk totals from the input); returns the previous bound."""
+    return int(lib().axon_scan_poll_bound(int(polls)))
 
 
 def copy(src, dst) -> None:

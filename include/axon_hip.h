@@ -23,7 +23,12 @@
  *       `input_specs` order, outputs in `out_0..out_k` order);
  *   axon_copy
  *       no counterpart in the reference: a plain device copy of known size
- *       used to calibrate HBM traffic counters.
+ *       used to calibrate HBM traffic counters;
+ *   axon_scan_poll_bound
+ *       no counterpart in the reference (whose scan is a sequential carry,
+ *       winners/cumsum_llama3_vocab.py:57-75): sets how long the single-pass
+ *       cumsum variant waits for an earlier chunk's published total before
+ *       recomputing it from the input.
  *
  * Conventions: every call returns AXON_OK (0) or an AXON_E* code, and never
  * throws; `axon_last_error` gives the calling thread's last message. Device
@@ -108,8 +113,8 @@ int axon_variant_check(const char* kernel, int hw_variant,
 
 /* Bytes of device workspace one launch needs (0 for most variants). A
  * workspace must be zero-filled before its first launch; every launch leaves
- * it ready for the next one (the single-pass cumsum variant keeps an error
- * word there, set only if a poll bound ran out). Launches that overlap on one
+ * it ready for the next one (the single-pass cumsum variant keeps a count of
+ * recomputed chunk totals in its first word). Launches that overlap on one
  * workspace race. */
 size_t axon_variant_workspace(const char* kernel, int hw_variant,
                               const int32_t* tiles, int n_tiles,
@@ -133,6 +138,13 @@ int axon_variant_launch(const char* kernel, int hw_variant,
  * with a plain vector-copy kernel: the known-size reference for traffic
  * counters. */
 int axon_copy(const void* src, void* dst, size_t bytes, axon_stream_t stream);
+
+/* Single-pass cumsum (hw variant 2 of "cumsum" and "cumsum_probs"): a chunk
+ * polls each earlier chunk's published total at most `polls` times (default
+ * 4096), then recomputes the missing total from the input, so the result is
+ * the same for every bound, including 0 (always recompute). Process-wide;
+ * applies to launches enqueued after the call. Returns the previous bound. */
+uint32_t axon_scan_poll_bound(uint32_t polls);
 
 #ifdef __cplusplus
 }

@@ -1,5 +1,5 @@
 """Spec `attention`: fused QKV projection + single-head attention with a bare
-exp / sum softmax and no scale (the reference's kernels/attention/__init__.py:14-36):
+exp / sum softmax and no scale (the reference's kernels/attention/__init__.py:15-35):
 q, k, v = x w_q, x w_k, x w_v; out = softmax(q kᵀ) v."""
 
 from axon.kernel_spec import KernelSpec

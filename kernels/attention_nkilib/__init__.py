@@ -1,6 +1,6 @@
 """Spec `attention_nkilib`: single-head softmax(q @ k_t) @ v with k given
 transposed (d, s), no scale inside and no max subtraction
-(kernels/attention_nkilib/__init__.py:842-863 of the reference)."""
+(kernels/attention_nkilib/__init__.py:22-43 of the reference)."""
 
 from axon.kernel_spec import KernelSpec
 

@@ -1,5 +1,5 @@
 """Spec `cumsum`: inclusive prefix sum along the last axis
-(kernels/cumsum/__init__.py:369-378 of the reference)."""
+(kernels/cumsum/__init__.py:15-24 of the reference)."""
 
 from axon.kernel_spec import KernelSpec
 

@@ -1,6 +1,6 @@
 """Spec `fused_adam`: Adam with L2 weight decay, no AMSGrad; three (p, 1)
 per-row scalars broadcast over the free axis
-(kernels/fused_adam/__init__.py:448-469 of the reference)."""
+(kernels/fused_adam/__init__.py:27-48 of the reference)."""
 
 from axon.kernel_spec import KernelSpec
 

@@ -1,6 +1,6 @@
 """Spec `layernorm`: bare LayerNorm over the last axis (no affine), eps 1e-6.
 
-Spec surface as in kernels/layernorm/__init__.py:100-109 of the reference."""
+Spec surface as in kernels/layernorm/__init__.py:16-25 of the reference."""
 
 from axon.kernel_spec import KernelSpec
 

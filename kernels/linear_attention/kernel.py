@@ -1,5 +1,5 @@
 """AxonArray statement of `linear_attention` (the reference's
-kernels/linear_attention/kernel.py:16-27): state = keyᵀ v, out = q state."""
+kernels/linear_attention/kernel.py:14-20): state = keyᵀ v, out = q state."""
 
 from axon import AxonArray
 

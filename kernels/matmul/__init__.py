@@ -1,5 +1,5 @@
-"""Spec `matmul`: x[m, k] @ w[k, n] (kernels/matmul/__init__.py:600-612 of
-the reference)."""
+"""Spec `matmul`: x[m, k] @ w[k, n] (the reference's kernels/matmul/__init__.py:13-25,
+math in kernels/matmul/kernel.py:7-8)."""
 
 from axon.kernel_spec import KernelSpec
 

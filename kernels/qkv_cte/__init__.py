@@ -1,7 +1,7 @@
 """Spec `qkv_cte`: the QKV context-encoding projection core, residual add ->
 RMSNorm (mean form, eps 1e-6, no gamma) -> projection,
     h = x + mlp_prev + attention_prev;  out = (h / sqrt(mean(h^2) + eps)) @ w,
-with the reference's dims, input names and order (kernels/qkv_cte/__init__.py:24-38
+with the reference's dims, input names and order (kernels/qkv_cte/__init__.py:23-37
 of the reference; M = tokens, K = hidden, N = fused QKV width)."""
 
 from axon.kernel_spec import KernelSpec

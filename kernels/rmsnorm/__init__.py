@@ -1,6 +1,6 @@
 """Spec `rmsnorm`: sum-form RMS normalisation of each row (no eps, no weight).
 
-Spec surface as in the reference's kernels/rmsnorm/__init__.py:17-26
+Spec surface as in the reference's kernels/rmsnorm/__init__.py:15-24
 (dim_vars (m, n), one input x[m, n], tile args M/N)."""
 
 from axon.kernel_spec import KernelSpec

@@ -1,5 +1,5 @@
 """Spec `rmsnorm_matmul`: (x / sqrt(sum x^2)) @ w, sum form without eps
-(kernels/rmsnorm_matmul/__init__.py:677-688 of the reference). The reference
+(kernels/rmsnorm_matmul/__init__.py:15-26 of the reference). The reference
 package has no `torch_ref`; this one adds it with the same math."""
 
 from axon.kernel_spec import KernelSpec

@@ -1,5 +1,5 @@
 """Spec `rope`: pointwise rotation on the d-major split layout
-(kernels/rope/__init__.py:190-208 of the reference): four inputs of shape
+(kernels/rope/__init__.py:15-33 of the reference): four inputs of shape
 (half_d, free), two outputs."""
 
 from axon.kernel_spec import KernelSpec

@@ -1,5 +1,5 @@
 """Spec `silu_mlp`: (silu(x @ w1) * (x @ w2)) @ w3
-(kernels/silu_mlp/__init__.py:754-772 of the reference). The reference
+(kernels/silu_mlp/__init__.py:16-34 of the reference). The reference
 package has no `torch_ref`; this one adds it with the same math."""
 
 from axon.kernel_spec import KernelSpec

@@ -23,9 +23,10 @@ def legal_tiles(name, variant, dims, codes, n_tiles, options=(1, 2, 4, 8, 16, 32
 
 
 def check_parity(name, sizes, *, rtol, atol, variants=None, budget=0, dtype=None,
-                 want=None, seed=42):
+                 want=None, seed=42, tiles=None):
     """Returns the number of (variant, tiles) keys checked; raises on the first
-    mismatch (message names the key)."""
+    mismatch (message names the key). `tiles` names one tile tuple to check
+    (it must be legal in every listed variant) instead of the legal set."""
     spec, dims, host = spec_inputs(name, sizes, dtype=dtype, seed=seed)
     dev = to_device(host)
     codes = [hip.dtype_code(t) for t in dev]
@@ -35,8 +36,12 @@ def check_parity(name, sizes, *, rtol, atol, variants=None, budget=0, dtype=None
     explicit = variants is not None
     variants = range(hip.variant_count(name)) if variants is None else variants
     checked = 0
+    only = tiles
     for v in variants:
         tiles = legal_tiles(name, v, dvals, codes, len(spec.tile_args))
+        if only is not None:
+            assert tuple(only) in tiles, f"{name} v{v}: tiles {tuple(only)} are not legal for {sizes}"
+            tiles = [tuple(only)]
         # A variant may not serve every shape (hw variant 2 of the plain GEMM
         # needs k % 64 == 0); asked for explicitly, it must.
         if not tiles and not explicit:
