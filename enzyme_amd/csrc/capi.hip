@@ -2,6 +2,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -130,6 +131,52 @@ __global__ __launch_bounds__(256) void copy_kernel(const uint4* __restrict__ src
         reinterpret_cast<u32x4*>(dst) + i);
 }
 
+// Workspace of axon_variant_launch_noalloc: one array per GPU, held for the
+// life of the process. Calls on one GPU share it (and race when they
+// overlap); it keeps the last call's contents, so the part a kernel needs at
+// zero is cleared before each launch.
+constexpr size_t kScratchBytes = size_t{32} << 20;
+static_assert(kScratchBytes % 16 == 0, "the zero fill writes whole 16-byte vectors");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current GPU's `scratch`, looked up once per device
+// (the array's name in host code is not a device address).
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error(std::string("hipGetDevice: ") + hipGetErrorString(e));
+    return AXON_EHIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("device index " + std::to_string(dev) + " beyond the scratch table");
+    return AXON_EHIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+      return AXON_EHIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return AXON_OK;
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(uint4* __restrict__ p, size_t n16) {
+  const uint4 z = {0u, 0u, 0u, 0u};
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    p[i] = z;
+}
+
 }  // namespace axon
 
 using namespace axon;
@@ -246,31 +293,34 @@ size_t axon_variant_workspace(const char* kernel, int hw_variant, const int32_t*
   return f->workspace(c);
 }
 
-int axon_variant_launch(const char* kernel, int hw_variant, const int32_t* tiles, int n_tiles,
-                        const int64_t* dims, int n_dims, const int32_t* dtypes, int n_dtypes,
-                        const void* const* inputs, int n_in, void* const* outputs, int n_out,
-                        void* workspace, size_t workspace_bytes, axon_stream_t stream) {
-  const Call c{hw_variant, tiles, n_tiles, dims, n_dims, dtypes, n_dtypes};
-  const Family* f = nullptr;
-  int rc = checked(kernel, c, &f);
-  if (rc != AXON_OK) return rc;
+}  // extern "C"
+
+namespace {
+
+// Argument checks shared by both launch entry points. Sets *empty when every
+// output has zero elements (the launch is then a no-op: empty tensors may
+// carry null data pointers).
+int check_launch_args(const Family* f, const Call& c, const void* const* inputs, int n_in,
+                      void* const* outputs, int n_out, bool* empty) {
   if (n_in != f->n_inputs || n_out != f->n_outputs || inputs == nullptr || outputs == nullptr) {
     set_error(std::string(f->name) + ": expected " + std::to_string(f->n_inputs) + " inputs and " +
               std::to_string(f->n_outputs) + " outputs");
     return AXON_EARG;
   }
-  // Every output empty: nothing to read or write (empty tensors may carry
-  // null data pointers), so the launch is a no-op.
+  *empty = false;
   OutDesc d[8];
   if (f->n_outputs <= 8) {
-    f->outputs(dims, dtypes, d);
-    bool empty = true;
+    f->outputs(c.dims, c.dtypes, d);
+    bool all_empty = true;
     for (int i = 0; i < f->n_outputs; ++i) {
       int64_t e = 1;
       for (int r = 0; r < d[i].rank; ++r) e *= d[i].shape[r];
-      empty = empty && e == 0;
+      all_empty = all_empty && e == 0;
     }
-    if (empty) return AXON_OK;
+    if (all_empty) {
+      *empty = true;
+      return AXON_OK;
+    }
   }
   for (int i = 0; i < n_in; ++i)
     if (inputs[i] == nullptr) {
@@ -282,6 +332,24 @@ int axon_variant_launch(const char* kernel, int hw_variant, const int32_t* tiles
       set_error(std::string(f->name) + ": output " + std::to_string(i) + " is null");
       return AXON_EARG;
     }
+  return AXON_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int axon_variant_launch(const char* kernel, int hw_variant, const int32_t* tiles, int n_tiles,
+                        const int64_t* dims, int n_dims, const int32_t* dtypes, int n_dtypes,
+                        const void* const* inputs, int n_in, void* const* outputs, int n_out,
+                        void* workspace, size_t workspace_bytes, axon_stream_t stream) {
+  const Call c{hw_variant, tiles, n_tiles, dims, n_dims, dtypes, n_dtypes};
+  const Family* f = nullptr;
+  int rc = checked(kernel, c, &f);
+  if (rc != AXON_OK) return rc;
+  bool empty = false;
+  rc = check_launch_args(f, c, inputs, n_in, outputs, n_out, &empty);
+  if (rc != AXON_OK || empty) return rc;
   const size_t need = f->workspace(c);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_error(std::string(f->name) + ": workspace of " + std::to_string(need) +
@@ -289,6 +357,45 @@ int axon_variant_launch(const char* kernel, int hw_variant, const int32_t* tiles
     return AXON_EWORKSPACE;
   }
   return f->launch(c, inputs, outputs, workspace, reinterpret_cast<hipStream_t>(stream));
+}
+
+int axon_variant_launch_noalloc(const char* kernel, int hw_variant, const int32_t* tiles,
+                                int n_tiles, const int64_t* dims, int n_dims,
+                                const int32_t* dtypes, int n_dtypes, const void* const* inputs,
+                                int n_in, void* const* outputs, int n_out, axon_stream_t stream) {
+  const Call c{hw_variant, tiles, n_tiles, dims, n_dims, dtypes, n_dtypes};
+  const Family* f = nullptr;
+  int rc = checked(kernel, c, &f);
+  if (rc != AXON_OK) return rc;
+  bool empty = false;
+  rc = check_launch_args(f, c, inputs, n_in, outputs, n_out, &empty);
+  if (rc != AXON_OK || empty) return rc;
+  const size_t need = f->workspace(c);
+  if (need > kScratchBytes) {
+    set_error(std::string(f->name) + " v" + std::to_string(hw_variant) + ": needs " +
+              std::to_string(need) + " bytes of workspace, above the " +
+              std::to_string(kScratchBytes) +
+              "-byte static workspace of axon_variant_launch_noalloc; use axon_variant_launch "
+              "with a caller workspace");
+    return AXON_EWORKSPACE;
+  }
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if (need > 0) {
+    rc = scratch_address(&ws);
+    if (rc != AXON_OK) return rc;
+    const size_t zero = f->workspace_zeroed != nullptr ? f->workspace_zeroed(c) : 0;
+    if (zero > 0) {
+      const size_t n16 = (zero + 15) / 16;  // within the array: kScratchBytes % 16 == 0
+      size_t blocks = (n16 + 255) / 256;
+      if (blocks > 1024) blocks = 1024;
+      hipLaunchKernelGGL(zero_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                         static_cast<uint4*>(ws), n16);
+      rc = launch_status("zero_kernel");
+      if (rc != AXON_OK) return rc;
+    }
+  }
+  return f->launch(c, inputs, outputs, ws, st);
 }
 
 int axon_copy(const void* src, void* dst, size_t bytes, axon_stream_t stream) {

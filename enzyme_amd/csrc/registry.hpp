@@ -59,6 +59,10 @@ struct Family {
   void (*outputs)(const int64_t* dims, const int32_t* dtypes, OutDesc* out);
   int (*launch)(const Call& c, const void* const* in, void* const* out, void* ws,
                 hipStream_t stream);
+  // Bytes at the start of the workspace that must hold zeros when it last
+  // served a different kernel (null: none; every byte is written before it
+  // is read).
+  size_t (*workspace_zeroed)(const Call& c) = nullptr;
 };
 
 // Records `msg` as the calling thread's last error.

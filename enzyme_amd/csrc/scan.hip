@@ -412,6 +412,11 @@ size_t workspace_scan(const Call& c) {
   return c.variant == 1 ? slots : kOnepassHeader + slots;
 }
 
+// The single-pass variant's slots must not hold a word whose tag matches the
+// launch: zero the whole workspace when it held anything but this variant's
+// own words.
+size_t zeroed_scan(const Call& c) { return c.variant == 2 ? workspace_scan(c) : 0; }
+
 void outputs_scan(const int64_t* dims, const int32_t* dtypes, OutDesc* out) {
   out[0] = {2, {dims[0], dims[1]}, dtypes[0]};
 }
@@ -503,13 +508,13 @@ unsigned set_scan_poll_bound(unsigned polls) {
 
 const Family* family_cumsum() {
   static const Family f = {"cumsum", 3, 1, 1, 2, kTileArgs, 2, summary_scan, manifest_scan,
-                           check_scan, workspace_scan, outputs_scan, launch_scan};
+                           check_scan, workspace_scan, outputs_scan, launch_scan, zeroed_scan};
   return &f;
 }
 
 const Family* family_cumsum_probs() {
   static const Family f = {"cumsum_probs", 3, 1, 1, 2, kTileArgs, 2, summary_scan, manifest_scan,
-                           check_scan, workspace_scan, outputs_scan, launch_scan};
+                           check_scan, workspace_scan, outputs_scan, launch_scan, zeroed_scan};
   return &f;
 }
 

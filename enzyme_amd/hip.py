@@ -59,6 +59,7 @@ EXPORTED_SYMBOLS = (
     "axon_variant_check",
     "axon_variant_workspace",
     "axon_variant_launch",
+    "axon_variant_launch_noalloc",
     "axon_copy",
     "axon_scan_poll_bound",
 )
@@ -116,6 +117,12 @@ def _declare(lib: ctypes.CDLL) -> None:
             [ctypes.c_char_p, ctypes.c_int, _i32p, ctypes.c_int, _i64p, ctypes.c_int,
              _i32p, ctypes.c_int, _voidpp, ctypes.c_int, _voidpp, ctypes.c_int,
              ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+        ),
+        "axon_variant_launch_noalloc": (
+            ctypes.c_int,
+            [ctypes.c_char_p, ctypes.c_int, _i32p, ctypes.c_int, _i64p, ctypes.c_int,
+             _i32p, ctypes.c_int, _voidpp, ctypes.c_int, _voidpp, ctypes.c_int,
+             ctypes.c_void_p],
         ),
         "axon_copy": (
             ctypes.c_int,
@@ -272,8 +279,13 @@ class Launcher:
         inputs: Sequence[Any],
         input_shapes: Sequence[tuple[int, ...]] | None = None,
         outputs_: Sequence[Any] | None = None,
+        noalloc: bool = False,
     ):
+        """`noalloc=True` launches through axon_variant_launch_noalloc: no
+        workspace is allocated here, the library's static per-GPU array
+        serves as the kernels' workspace."""
         torch = _torch()
+        self.noalloc = bool(noalloc)
         self.kernel = kernel
         self.hw_variant = int(hw_variant)
         self.tiles = [int(t) for t in tiles]
@@ -309,9 +321,10 @@ class Launcher:
                 if tuple(t.shape) != d.shape or dtype_code(t) != d.dtype or not t.is_contiguous():
                     raise HipLibraryError(f"{kernel}: output {i} must be contiguous {d.shape}")
             self.outputs = list(outputs_)
-        ws = workspace_bytes(kernel, self.hw_variant, self.tiles, self.dims, self.dtypes)
-        # A workspace starts zero-filled (split-K tile counters start at zero;
-        # every launch leaves them at zero again).
+        ws = 0 if self.noalloc else workspace_bytes(kernel, self.hw_variant, self.tiles, self.dims,
+                                                    self.dtypes)
+        # A caller workspace starts zero-filled (every launch leaves it ready
+        # for the next one).
         self.workspace = torch.zeros(ws, dtype=torch.uint8, device=device) if ws else None
         self._pack()
 
@@ -340,12 +353,19 @@ class Launcher:
     def launch(self, stream: Any = None) -> None:
         torch = _torch()
         s = stream if stream is not None else torch.cuda.current_stream(self.inputs[0].device)
-        rc = lib().axon_variant_launch(
-            self._c_kernel, self.hw_variant, self._c_tiles, len(self.tiles), self._c_dims,
-            len(self.dims), self._c_dtypes, len(self.dtypes), self._c_in, len(self.inputs),
-            self._c_out, len(self.outputs), self._c_ws, self._c_ws_bytes,
-            ctypes.c_void_p(s.cuda_stream),
-        )
+        if self.noalloc:
+            rc = lib().axon_variant_launch_noalloc(
+                self._c_kernel, self.hw_variant, self._c_tiles, len(self.tiles), self._c_dims,
+                len(self.dims), self._c_dtypes, len(self.dtypes), self._c_in, len(self.inputs),
+                self._c_out, len(self.outputs), ctypes.c_void_p(s.cuda_stream),
+            )
+        else:
+            rc = lib().axon_variant_launch(
+                self._c_kernel, self.hw_variant, self._c_tiles, len(self.tiles), self._c_dims,
+                len(self.dims), self._c_dtypes, len(self.dtypes), self._c_in, len(self.inputs),
+                self._c_out, len(self.outputs), self._c_ws, self._c_ws_bytes,
+                ctypes.c_void_p(s.cuda_stream),
+            )
         if rc != AXON_OK:
             _raise(rc, f"launch({self.kernel}, v{self.hw_variant}, tiles {self.tiles})")
 

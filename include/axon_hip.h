@@ -134,6 +134,26 @@ int axon_variant_launch(const char* kernel, int hw_variant,
                         void* workspace, size_t workspace_bytes,
                         axon_stream_t stream);
 
+/* As axon_variant_launch, but allocates nothing and takes no workspace. No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The kernels' workspace is a static device
+ * array of 32 MiB per GPU, held until the process ends; a launch that needs
+ * more returns AXON_EWORKSPACE (sizes in axon_last_error()) and enqueues
+ * nothing. The first call on a device looks the array's address up
+ * (hipGetSymbolAddress); no call allocates or frees memory. Every call on a
+ * GPU shares that GPU's array and it keeps the last call's contents: the part
+ * a kernel needs at zero is cleared by a small fill kernel on `stream` before
+ * the launch. Calls whose execution can overlap on one GPU (unordered streams,
+ * or several threads) race. */
+int axon_variant_launch_noalloc(const char* kernel, int hw_variant,
+                                const int32_t* tiles, int n_tiles,
+                                const int64_t* dims, int n_dims,
+                                const int32_t* dtypes, int n_dtypes,
+                                const void* const* inputs, int n_in,
+                                void* const* outputs, int n_out,
+                                axon_stream_t stream);
+
 /* Copy `bytes` (a multiple of 16, both pointers 16-byte aligned) on `stream`
  * with a plain vector-copy kernel: the known-size reference for traffic
  * counters. */
