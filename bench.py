@@ -18,10 +18,12 @@ are behind it: after an idle second (the CPU baseline legs leave the GPU
 idle) the clocks take about 30 ms of back-to-back launches to settle, and a
 launch count alone (the 33 us matmul runs its first launches at 240 us and
 its next 25 at 42 us) would time the ramp. The settle each workload got is
-reported (`settle_ms`, `settle_launches`). Then exactly `--steps` launches
-run between two HIP events recorded on the stream the kernels are launched
-on, bracketed by device syncs; the average launch duration is the elapsed
-time / steps.
+reported (`settle_ms`, `settle_launches`). Then exactly `--steps` launches,
+captured into one HIP graph, are replayed once between two HIP events on the
+stream, bracketed by device syncs; the average launch duration is the
+elapsed time / steps. The graph keeps the host's per-launch cost (Python,
+ctypes, argument checks: several microseconds) out of the measurement of
+kernels that themselves take only 6-16 us.
 
 Correctness: after timing, each workload's outputs are filled with NaN, the
 kernel is launched once more, and the result is compared with the oracle
@@ -77,7 +79,7 @@ CONFIGS = [
         label="RoPE Llama-3-8B: q[1,4096,32,128] k[1,4096,8,128] bf16, cos/sin[4096,128] fp32, theta 500000",
     ),
     dict(
-        spec="rmsnorm_weighted", sizes=(2048, 4096), variant=0, tiles=(2, 2), bound="hbm",
+        spec="rmsnorm_weighted", sizes=(2048, 4096), variant=0, tiles=(1, 8), bound="hbm",
         work=33_562_624, rtol=1e-2, atol=1e-2,
         label="RMSNorm x[2048,4096] bf16, weight[4096] bf16, eps 1e-6",
     ),
@@ -123,38 +125,62 @@ def load_spec(name: str):
 def timed_launches(launch, n_sets: int, steps: int, warmup: int, settle_ms: float, stream):
     """Settle the clocks, then time `steps` back-to-back launches.
 
-    `launch(i)` enqueues one launch on buffer set i on `stream`. Untimed
-    launches run first until at least `warmup` of them and `settle_ms` of
-    device time (HIP events on `stream`) are behind; the chunks double so the
-    last one covers at least half the settle period without host gaps.
-    Returns (average us per timed launch, settle ms, settle launches)."""
+    `launch(i)` enqueues one launch on buffer set i on torch's current stream.
+    Untimed launches run first on `stream` until at least `warmup` of them and
+    `settle_ms` of device time (HIP events on `stream`) are behind; the chunks
+    double so the last one covers at least half the settle period. The timed
+    launches are captured into one HIP graph (capture only records; nothing
+    runs) and the graph is replayed once between two HIP events on `stream`,
+    so the host's per-launch cost (Python, ctypes, argument checks) cannot
+    leave the GPU idle between launches of a few-microsecond kernel. Each
+    captured launch is an ordinary kernel node over its own buffer set; the
+    single-pass scan's launch tags are fresh on this first replay. Returns
+    (average us per timed launch, settle ms, settle launches)."""
     import torch
 
     w0 = torch.cuda.Event(enable_timing=True)
     w1 = torch.cuda.Event(enable_timing=True)
-    w0.record(stream)
-    done = 0
-    for _ in range(max(0, warmup)):
-        launch(done % n_sets)
-        done += 1
-    w1.record(stream)
-    torch.cuda.synchronize()
-    chunk = max(1, done)
-    while w0.elapsed_time(w1) < settle_ms and done < MAX_SETTLE_LAUNCHES:
-        for _ in range(chunk):
+    with torch.cuda.stream(stream):
+        w0.record(stream)
+        done = 0
+        for _ in range(max(0, warmup)):
             launch(done % n_sets)
             done += 1
         w1.record(stream)
         torch.cuda.synchronize()
-        chunk *= 2
+        chunk = max(1, done)
+        while w0.elapsed_time(w1) < settle_ms and done < MAX_SETTLE_LAUNCHES:
+            for _ in range(chunk):
+                launch(done % n_sets)
+                done += 1
+            w1.record(stream)
+            torch.cuda.synchronize()
+            chunk *= 2
     settled = w0.elapsed_time(w1)
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(steps):
-        launch((done + i) % n_sets)
-    end.record(stream)
-    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            launch((done + i) % n_sets)
+    # The capture left the GPU idle for a moment: a short eager burst
+    # (2 ms of launches) brings the clocks back before the replay.
+    with torch.cuda.stream(stream):
+        w0.record(stream)
+        burst = 0
+        while True:
+            for _ in range(max(1, n_sets)):
+                launch(burst % n_sets)
+                burst += 1
+            w1.record(stream)
+            torch.cuda.synchronize()
+            if w0.elapsed_time(w1) >= 2.0 or burst >= MAX_SETTLE_LAUNCHES:
+                break
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+    del graph
     return start.elapsed_time(end) * 1e3 / steps, settled, done
 
 
@@ -184,7 +210,7 @@ def measure(cfg: dict, steps: int, warmup: int, settle_ms: float):
     ]
     stream = torch.cuda.current_stream()
     avg_us, settled, launches = timed_launches(
-        lambda i: sets[i].launch(stream), n_sets, steps, warmup, settle_ms, stream)
+        lambda i: sets[i].launch(), n_sets, steps, warmup, settle_ms, stream)
     for o in first.outputs:
         o.fill_(float("nan"))
     first.launch(stream)
@@ -195,10 +221,11 @@ def measure(cfg: dict, steps: int, warmup: int, settle_ms: float):
     return avg_us, settled, launches, outs, host
 
 
-def measure_copy(nbytes: int, steps: int, warmup: int, settle_ms: float) -> float:
-    """Average duration (us) of a plain 16-byte-vector device copy that reads
-    and writes `nbytes` each, rotating over >= 1 GiB of buffer pairs: the
-    practical HBM ceiling for a kernel moving 2 * nbytes."""
+def measure_copy(nbytes: int, steps: int, warmup: int, settle_ms: float):
+    """The fastest plain device copy reading and writing `nbytes` each, over
+    every launch shape of hip.COPY_SHAPES, rotating over >= 1 GiB of buffer
+    pairs: the practical HBM ceiling for a streaming kernel moving 2 * nbytes.
+    Returns (best us, best shape, {shape: us})."""
     import torch
 
     from enzyme_amd import hip
@@ -208,10 +235,15 @@ def measure_copy(nbytes: int, steps: int, warmup: int, settle_ms: float) -> floa
     sets = [(torch.empty(nbytes, dtype=torch.uint8, device="cuda"),
              torch.empty(nbytes, dtype=torch.uint8, device="cuda")) for _ in range(n_sets)]
     stream = torch.cuda.current_stream()
-    us, _, _ = timed_launches(lambda i: hip.copy(*sets[i]), n_sets, steps, warmup, settle_ms, stream)
+    by_shape = {}
+    for shape in sorted(hip.COPY_SHAPES):
+        us, _, _ = timed_launches(lambda i, sh=shape: hip.copy(*sets[i], shape=sh), n_sets, steps,
+                                  warmup, settle_ms, stream)
+        by_shape[shape] = round(us, 3)
     del sets
     torch.cuda.empty_cache()
-    return us
+    best = min(by_shape, key=by_shape.get)
+    return by_shape[best], best, by_shape
 
 
 def oracle_outputs(cfg: dict, host):
@@ -319,8 +351,10 @@ def main(argv=None) -> int:
             row["mfma"] = {"achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                            "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
         if cfg["bound"] == "hbm":
-            cu = measure_copy(cfg["work"] // 2, args.steps, args.warmup, args.settle_ms)
+            cu, shape, by_shape = measure_copy(cfg["work"] // 2, args.steps, args.warmup, args.settle_ms)
             row["copy_us"] = round(cu, 3)
+            row["copy_shape"] = shape
+            row["copy_us_by_shape"] = by_shape
             row["vs_copy"] = round(cu / us, 4)
         row.update(verdict(cfg, outs, oracle_outputs(cfg, host)))
         if not args.no_cpu:
@@ -363,9 +397,10 @@ def main(argv=None) -> int:
             "us": hrow["copy_us"],
             "achieved": round(head["work"] / (hrow["copy_us"] * 1e-6) / 1e9, 2),
             "unit": "GB/s",
-            "what": "plain 16-byte-vector copy reading and writing half the headline's algorithmic "
-                    "bytes each, same buffer rotation: the HBM rate a streaming kernel of this size "
-                    "reaches here",
+            "shape": hrow["copy_shape"],
+            "what": "fastest of four plain 16-byte-vector copy launch shapes reading and writing half "
+                    "the headline's algorithmic bytes each, same buffer rotation: the HBM rate a "
+                    "streaming kernel of this size reaches here",
         },
     }
     if "cpu_ms" in hrow:

@@ -131,6 +131,25 @@ __global__ __launch_bounds__(256) void copy_kernel(const uint4* __restrict__ src
         reinterpret_cast<u32x4*>(dst) + i);
 }
 
+// One-shot copy: every thread moves V vectors (its loads all in flight
+// before its stores), one block per 256 * V vectors.
+template <int V>
+__global__ __launch_bounds__(256) void copy_oneshot_kernel(const uint4* __restrict__ src,
+                                                          uint4* __restrict__ dst, size_t n16) {
+  const size_t base = static_cast<size_t>(blockIdx.x) * blockDim.x * V + threadIdx.x;
+  u32x4 r[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const size_t i = base + static_cast<size_t>(v) * blockDim.x;
+    r[v] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + (i < n16 ? i : 0));
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const size_t i = base + static_cast<size_t>(v) * blockDim.x;
+    if (i < n16) __builtin_nontemporal_store(r[v], reinterpret_cast<u32x4*>(dst) + i);
+  }
+}
+
 // Workspace of axon_variant_launch_noalloc: one array per GPU, held for the
 // life of the process. Calls on one GPU share it (and race when they
 // overlap); it keeps the last call's contents, so the part a kernel needs at
@@ -399,17 +418,42 @@ int axon_variant_launch_noalloc(const char* kernel, int hw_variant, const int32_
 }
 
 int axon_copy(const void* src, void* dst, size_t bytes, axon_stream_t stream) {
+  return axon_copy_shape(src, dst, bytes, 0, stream);
+}
+
+int axon_copy_shape(const void* src, void* dst, size_t bytes, int shape, axon_stream_t stream) {
   if (src == nullptr || dst == nullptr || (bytes & 15u) || !aligned16(src) || !aligned16(dst)) {
     set_error("axon_copy: pointers must be 16-byte aligned and bytes a multiple of 16");
     return AXON_EARG;
   }
+  if (shape < 0 || shape > 3) {
+    set_error("axon_copy_shape: shape must be 0..3");
+    return AXON_EARG;
+  }
   if (bytes == 0) return AXON_OK;
   const size_t n16 = bytes / 16;
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const uint4* s = static_cast<const uint4*>(src);
+  uint4* d = static_cast<uint4*>(dst);
+  if (shape == 1 || shape == 2) {
+    const int V = shape == 1 ? 8 : 4;
+    const size_t blocks = (n16 + 256 * V - 1) / (256 * V);
+    if (blocks > 0x7fffffffu) {
+      set_error("axon_copy_shape: copy too large for a one-shot grid");
+      return AXON_EARG;
+    }
+    if (V == 8)
+      hipLaunchKernelGGL(copy_oneshot_kernel<8>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                         st, s, d, n16);
+    else
+      hipLaunchKernelGGL(copy_oneshot_kernel<4>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                         st, s, d, n16);
+    return launch_status("copy_oneshot_kernel");
+  }
   size_t blocks = (n16 + 255) / 256;
-  if (blocks > 256 * 64) blocks = 256 * 64;
-  hipLaunchKernelGGL(copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint4*>(src),
-                     static_cast<uint4*>(dst), n16);
+  const size_t cap = shape == 0 ? 256 * 64 : 1024;
+  if (blocks > cap) blocks = cap;
+  hipLaunchKernelGGL(copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, s, d, n16);
   return launch_status("copy_kernel");
 }
 

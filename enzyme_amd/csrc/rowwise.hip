@@ -45,33 +45,45 @@ __global__ __launch_bounds__(1024) void rowwise_kernel(const T* __restrict__ x,
   const bool live = row < m;
   const T* xr = x + (live ? row : 0) * n;
   T* yr = y + (live ? row : 0) * n;
+  auto offset = [&](int v) -> int64_t {
+    return (static_cast<int64_t>(v * Wr + wr) * kWave + lane) * E;
+  };
 
-  float xv[V][E];
-  bool ok[V][E];
+  // The row stays in registers as loaded (16-byte vectors; elements are
+  // widened to fp32 where they are used). Aligned rows (n % E == 0) load
+  // branch-free: a vector past the row re-reads the row's first one and is
+  // masked, so the V loads, and the weight's, are all in flight together.
+  Vec<T> xraw[V];
+  bool vin[V];
+  Vec<T> wraw[MODE == kRmsWeighted ? V : 1];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
-    const int64_t off = (static_cast<int64_t>(v * Wr + wr) * kWave + lane) * E;
+    const int64_t off = offset(v);
     if constexpr (ALIGNED) {
-      const bool in = live && off < n;  // n % E == 0, so a vector is all-in or all-out
-      if (in) {
-        Vec<T> t = load_vec_nt(xr + off);  // streamed once: bypass cache allocation
-#pragma unroll
-        for (int e = 0; e < E; ++e) xv[v][e] = to_f32(t.v[e]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < E; ++e) xv[v][e] = 0.f;
-      }
-#pragma unroll
-      for (int e = 0; e < E; ++e) ok[v][e] = in;
+      vin[v] = live && off < n;
+      if constexpr (MODE == kRmsWeighted) wraw[v] = load_vec(w + (off < n ? off : 0));
+      xraw[v] = load_vec_nt(xr + (vin[v] ? off : 0));  // streamed once
     } else {
+      vin[v] = live;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const bool in = live && off + e < n;
-        ok[v][e] = in;
-        xv[v][e] = in ? to_f32(xr[off + e]) : 0.f;
+        xraw[v].v[e] = in ? xr[off + e] : from_f32<T>(0.f);
+        if constexpr (MODE == kRmsWeighted) wraw[v].v[e] = w[off + e < n ? off + e : 0];
       }
     }
   }
+  // Keep the scheduler from sinking the weight loads past the reduction.
+  __builtin_amdgcn_sched_barrier(0);
+  // Element (v, e) as fp32, 0 outside the row.
+  auto xat = [&](int v, int e) -> float {
+    if constexpr (ALIGNED) return vin[v] ? to_f32(xraw[v].v[e]) : 0.f;
+    return to_f32(xraw[v].v[e]);  // out-of-row elements were loaded as 0
+  };
+  auto in_row = [&](int v, int e) -> bool {
+    if constexpr (ALIGNED) return vin[v];
+    return vin[v] && offset(v) + e < n;
+  };
 
   // Row total of one per-lane partial: wave butterfly, then LDS across waves.
   auto row_total = [&](float part, int slot) -> float {
@@ -91,7 +103,7 @@ __global__ __launch_bounds__(1024) void rowwise_kernel(const T* __restrict__ x,
 #pragma unroll
     for (int v = 0; v < V; ++v)
 #pragma unroll
-      for (int e = 0; e < E; ++e) s += xv[v][e] * xv[v][e];
+      for (int e = 0; e < E; ++e) s += xat(v, e) * xat(v, e);
     const float tot = row_total(s, 0);
     if constexpr (MODE == kRmsSum) {
       scale = 1.f / sqrtf(tot);
@@ -103,63 +115,49 @@ __global__ __launch_bounds__(1024) void rowwise_kernel(const T* __restrict__ x,
 #pragma unroll
     for (int v = 0; v < V; ++v)
 #pragma unroll
-      for (int e = 0; e < E; ++e) s += xv[v][e];
+      for (int e = 0; e < E; ++e) s += xat(v, e);
     const float mean = row_total(s, 0) / static_cast<float>(n);
     float q = 0.f;
 #pragma unroll
     for (int v = 0; v < V; ++v)
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        const float d = ok[v][e] ? xv[v][e] - mean : 0.f;
+        const float d = in_row(v, e) ? xat(v, e) - mean : 0.f;
         q += d * d;
       }
     const float var = row_total(q, 1) / static_cast<float>(n);
     scale = 1.f / sqrtf(var + kNormEps);
     shift = mean;
-  } else {  // softmax
+  } else {  // softmax: exp is recomputed for the output (cheaper than holding it)
     float s = 0.f;
 #pragma unroll
     for (int v = 0; v < V; ++v)
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        xv[v][e] = ok[v][e] ? __expf(xv[v][e]) : 0.f;
-        s += xv[v][e];
-      }
+      for (int e = 0; e < E; ++e) s += in_row(v, e) ? __expf(xat(v, e)) : 0.f;
     scale = 1.f / row_total(s, 0);
   }
 
 #pragma unroll
   for (int v = 0; v < V; ++v) {
-    const int64_t off = (static_cast<int64_t>(v * Wr + wr) * kWave + lane) * E;
-    float wv[E];
-    if constexpr (MODE == kRmsWeighted) {
-      if constexpr (ALIGNED) {
-        const Vec<T> t = load_vec(w + (off < n ? off : 0));
-#pragma unroll
-        for (int e = 0; e < E; ++e) wv[e] = to_f32(t.v[e]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < E; ++e) wv[e] = to_f32(w[off + e < n ? off + e : 0]);
-      }
-    }
-    float o[E];
+    const int64_t off = offset(v);
+    Vec<T> o;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      float t = (xv[v][e] - shift) * scale;
-      if constexpr (MODE == kRmsWeighted) t *= wv[e];
-      o[e] = t;
+      float t;
+      if constexpr (MODE == kSoftmax) {
+        t = __expf(xat(v, e)) * scale;
+      } else {
+        t = (xat(v, e) - shift) * scale;
+        if constexpr (MODE == kRmsWeighted) t *= to_f32(wraw[v].v[e]);
+      }
+      o.v[e] = from_f32<T>(t);
     }
     if constexpr (ALIGNED) {
-      if (live && off < n) {
-        Vec<T> t;
-#pragma unroll
-        for (int e = 0; e < E; ++e) t.v[e] = from_f32<T>(o[e]);
-        store_vec_nt(yr + off, t);
-      }
+      if (vin[v]) store_vec_nt(yr + off, o);
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e)
-        if (ok[v][e]) yr[off + e] = from_f32<T>(o[e]);
+        if (in_row(v, e)) yr[off + e] = o.v[e];
     }
   }
 }

@@ -59,14 +59,14 @@ __device__ __forceinline__ void load_striped(const T* __restrict__ row, int64_t 
   for (int v = 0; v < V; ++v) {
     const int64_t off = wbase + static_cast<int64_t>(v * kWave + lane) * E;
     if constexpr (ALIGNED) {
-      if (off < n) {  // n % E == 0: a vector is all in or all out
-        const Vec<T> t = NT ? load_vec_nt(row + off) : load_vec(row + off);
+      // n % E == 0: a vector is all in or all out. Branch-free (a vector past
+      // n re-reads the row's first one and is zeroed), so the V loads are in
+      // flight together.
+      const bool in = off < n;
+      const int64_t at = in ? off : 0;
+      const Vec<T> t = NT ? load_vec_nt(row + at) : load_vec(row + at);
 #pragma unroll
-        for (int e = 0; e < E; ++e) x[v][e] = to_f32(t.v[e]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < E; ++e) x[v][e] = 0.f;
-      }
+      for (int e = 0; e < E; ++e) x[v][e] = in ? to_f32(t.v[e]) : 0.f;
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) x[v][e] = off + e < n ? to_f32(row[off + e]) : 0.f;

@@ -61,6 +61,7 @@ EXPORTED_SYMBOLS = (
     "axon_variant_launch",
     "axon_variant_launch_noalloc",
     "axon_copy",
+    "axon_copy_shape",
     "axon_scan_poll_bound",
 )
 
@@ -127,6 +128,10 @@ def _declare(lib: ctypes.CDLL) -> None:
         "axon_copy": (
             ctypes.c_int,
             [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+        ),
+        "axon_copy_shape": (
+            ctypes.c_int,
+            [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p],
         ),
         "axon_scan_poll_bound": (ctypes.c_uint32, [ctypes.c_uint32]),
     }
@@ -396,16 +401,25 @@ def scan_poll_bound(polls: int) -> int:
     return int(lib().axon_scan_poll_bound(int(polls)))
 
 
-def copy(src, dst) -> None:
-    """Plain device copy (the traffic-counter calibration kernel)."""
+COPY_SHAPES = {
+    0: "one 16-byte vector per thread, grid-stride over <= 16384 blocks of 256",
+    1: "one-shot, 8 vectors per thread",
+    2: "one-shot, 4 vectors per thread",
+    3: "one 16-byte vector per thread, grid-stride over 1024 blocks of 256",
+}
+
+
+def copy(src, dst, shape: int = 0) -> None:
+    """Plain device copy (the traffic-counter calibration kernel) in one of
+    the launch shapes of COPY_SHAPES."""
     torch = _torch()
     nbytes = src.numel() * src.element_size()
     if dst.numel() * dst.element_size() != nbytes:
         raise HipLibraryError("copy: size mismatch")
     s = torch.cuda.current_stream(src.device)
-    rc = lib().axon_copy(
-        ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), nbytes,
+    rc = lib().axon_copy_shape(
+        ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), nbytes, int(shape),
         ctypes.c_void_p(s.cuda_stream),
     )
     if rc != AXON_OK:
-        _raise(rc, "axon_copy")
+        _raise(rc, "axon_copy_shape")

@@ -21,9 +21,10 @@
  *       running the compiled kernel on device buffers with its tile values
  *       baked in (src/axon/bench_runner.py:144-223: inputs by name in
  *       `input_specs` order, outputs in `out_0..out_k` order);
- *   axon_copy
+ *   axon_copy / axon_copy_shape
  *       no counterpart in the reference: a plain device copy of known size
- *       used to calibrate HBM traffic counters;
+ *       used to calibrate HBM traffic counters and to measure the fastest
+ *       copy of a given size;
  *   axon_scan_poll_bound
  *       no counterpart in the reference (whose scan is a sequential carry,
  *       winners/cumsum_llama3_vocab.py:57-75): sets how long the single-pass
@@ -156,8 +157,17 @@ int axon_variant_launch_noalloc(const char* kernel, int hw_variant,
 
 /* Copy `bytes` (a multiple of 16, both pointers 16-byte aligned) on `stream`
  * with a plain vector-copy kernel: the known-size reference for traffic
- * counters. */
+ * counters. Same as axon_copy_shape with shape 0. */
 int axon_copy(const void* src, void* dst, size_t bytes, axon_stream_t stream);
+
+/* The same copy in one of four launch shapes, to measure the fastest plain
+ * copy of a given size (the HBM ceiling a streaming kernel of that size can
+ * reach): 0 = one 16-byte vector per thread per step, grid-stride over at
+ * most 16384 blocks of 256; 1 = one-shot, 8 vectors per thread (all loads
+ * in flight before the stores); 2 = one-shot, 4 vectors per thread; 3 = as 0
+ * over 1024 blocks. No counterpart in the reference. */
+int axon_copy_shape(const void* src, void* dst, size_t bytes, int shape,
+                    axon_stream_t stream);
 
 /* Single-pass cumsum (hw variant 2 of "cumsum" and "cumsum_probs"): a chunk
  * polls each earlier chunk's published total at most `polls` times (default
