@@ -267,9 +267,9 @@ def test_bench_failure_is_one_terminal_row(tmp_path, monkeypatch):
 
 
 def test_correctness_column_from_outputs(tmp_path, monkeypatch):
-    """A device result is checked against the spec's baseline_op and torch_ref
-    on the same seeded inputs: the exact answer is correct, a perturbed one
-    is not, and max_abs_err records the gap."""
+    """A device result is checked against the spec's torch_ref on the same
+    seeded inputs: the exact answer is correct, a perturbed one is not, and
+    max_abs_err records the gap."""
     import numpy as np
 
     from enzyme_amd.dtypes import to_f32_numpy
@@ -290,6 +290,39 @@ def test_correctness_column_from_outputs(tmp_path, monkeypatch):
         r = rows_of(paths.results)[0]
         assert r["correct"] == want
         assert (float(r["max_abs_err"]) > 0.4) == (label == "bad")
+
+
+def test_correctness_decided_by_torch_ref_when_present(tmp_path, monkeypatch):
+    """cumsum at 128 x 32768 on N(0,1) inputs: the exact prefix sums
+    (torch.cumsum, double accumulation) are correct at the case tolerance
+    1e-3, although the reference's numpy baseline_op (sequential fp32) is
+    more than 1e-3 away from them; an output off the exact sums by 5e-3 is
+    not correct."""
+    import numpy as np
+    import torch
+
+    from enzyme_amd.kernel_spec import SEED
+
+    monkeypatch.chdir(tmp_path)
+    spec = dataclasses.replace(load_spec("cumsum"), tile_options=(1,))
+    dims = {"m": 128, "n": 32768}
+    (x,) = spec.make_inputs(**dims, rng=np.random.default_rng(SEED))
+    exact = torch.cumsum(torch.as_tensor(x), dim=-1).numpy()
+    assert np.abs(spec.baseline_op(x) - exact).max() > 1.5e-3
+    for label, out, want in (("exact", exact, "True"), ("off", exact + 5e-3, "False")):
+        paths = run_paths(spec, f"out/cumsum_{label}.csv")
+        paths.run_dir.mkdir(parents=True, exist_ok=True)
+
+        def ben(args, out=out):
+            return BenchStats(1.0, 1.0, 1.0, 1.0, 0.0, outputs=(out,))
+
+        install(monkeypatch, ok_compile, ben)
+        bench_runner.run_hip_bench(
+            spec, dims, hw_variant=0, tile_variant=0,
+            module_path=str(paths.variant_module("cumsum", 0, 0)), function_name="cumsum",
+            warmup=1, bench=1, paths=paths, rtol=1e-3, atol=1e-3, candidate_filter=False,
+        )
+        assert rows_of(paths.results)[0]["correct"] == want
 
 
 def test_torn_tail_is_truncated_before_append(tmp_path, monkeypatch):
