@@ -34,10 +34,17 @@
 // hw variant 1 gives each wave two 32-query tiles: every K and V^T fragment
 // read from LDS feeds two MFMAs, halving LDS reads per FLOP, at one wave per
 // SIMD (the second tile's accumulators fill the AGPRs).
+// hw variant 3 runs hw variant 2's schedule over split key ranges: the
+// grid adds a key-range index, each workgroup writes its range's
+// unnormalised O^T columns, running max and row sum to the workspace, and a
+// second kernel merges the ranges of each query row. It fills the GPU when
+// batch * heads * s is small (one head of 1024 queries is 8 workgroups of
+// 128 queries otherwise).
 // Tile arguments: TILES_IN_BLOCK_M = W / 4 (variant 0: 4 or 8 waves; variant
-//                 1: 4 waves), TILES_IN_BLOCK_N = BKV / 32 (variant 1: at
-//                 most 2); TILES_IN_BLOCK_K and TILES_IN_BLOCK_P are pinned
-//                 to 1.
+//                 1: 4 waves; variant 3: W / 2, 2, 4 or 8 waves),
+//                 TILES_IN_BLOCK_N = BKV / 32 (variants 1-3: at most 2);
+//                 TILES_IN_BLOCK_K = key-range splits (variant 3, 1 to 16;
+//                 otherwise pinned to 1); TILES_IN_BLOCK_P is pinned to 1.
 #include <atomic>
 #include <type_traits>
 
@@ -70,6 +77,13 @@ struct AttnArgs {
   int qblocks;
   int xcd_heads;     // heads per XCD when the XCD mapping applies, else 0
   float scale_log2;  // softmax scale * log2(e)
+  // Split key ranges (hw variant 3): nsplit ranges of kv_split keys each;
+  // partial results go to o_part [nsplit][bh][s][D] (unnormalised fp32) and
+  // ml_part [nsplit][bh][s][2] (running max in the exp2 domain, row sum).
+  int nsplit;
+  int kv_split;
+  float* o_part;
+  float* ml_part;
 };
 
 // Position of key k (0..15 inside its 16-key group) in a V^T row: bits 2 and
@@ -363,7 +377,7 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
 // V(j-1) left; one barrier per block. 4 or 8 waves of 32 queries. Causal:
 // a wave skips the compute of blocks past its last query (it still stages
 // K and V and meets the barrier with the others).
-template <int W, int TN, bool CAUSAL, bool KT>
+template <int W, int TN, bool CAUSAL, bool KT, bool SPLIT>
 __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
   constexpr int NT = W * 64;
   constexpr int BQ = 32 * W;
@@ -384,9 +398,13 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
   const int wave = tid >> 6;
   const int h = lane >> 5;
 
-  int rank, bh;
-  const int bid = static_cast<int>(blockIdx.x);
-  if (a.xcd_heads > 0) {
+  int rank, bh, sp = 0;
+  int bid = static_cast<int>(blockIdx.x);
+  if constexpr (SPLIT) {
+    sp = bid % a.nsplit;
+    bid /= a.nsplit;
+  }
+  if (!SPLIT && a.xcd_heads > 0) {
     const int x = bid % kXcds, j = bid / kXcds;
     rank = j / a.xcd_heads;
     bh = x + kXcds * (j % a.xcd_heads);
@@ -408,9 +426,13 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
   const int wq = wave < W / 2 ? wave : 3 * W / 2 - 1 - wave;
   const int qw = q0 + wq * 32;
   const int my_q = qw + (lane & 31);
-  const int kv_end = CAUSAL ? min(a.s, q0 + BQ) : a.s;
-  const int nblocks = (kv_end + BKV - 1) / BKV;
-  const int klast = max(nblocks - 1, 0) * BKV;
+  // Key range [kv_lo, kv_end) of this workgroup (the whole sequence unless
+  // the key range is split).
+  const int kv_lo = SPLIT ? sp * a.kv_split : 0;
+  int kv_end = CAUSAL ? min(a.s, q0 + BQ) : a.s;
+  if constexpr (SPLIT) kv_end = min(kv_end, kv_lo + a.kv_split);
+  const int nblocks = kv_end > kv_lo ? (kv_end - kv_lo + BKV - 1) / BKV : 0;
+  const int klast = kv_lo + max(nblocks - 1, 0) * BKV;
 
   bf16x8 qf[D / 16];
 #pragma unroll
@@ -536,7 +558,7 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
     constexpr bool MASK = decltype(mask_tag)::value;
     constexpr int P = decltype(par_tag)::value;
     floatx16 (&sacc)[TN] = acc_s[P];
-    const int kv0 = j * BKV;
+    const int kv0 = kv_lo + j * BKV;
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < TN; ++t)
@@ -578,10 +600,10 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
   };
 
   if (nblocks > 0) {
-    load_k(0);
+    load_k(kv_lo);
     store_k(0);
-    load_k(BKV);
-    load_v(0);
+    load_k(kv_lo + BKV);
+    load_v(kv_lo);
     store_k(1);
     store_v(0);
   }
@@ -589,9 +611,9 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
   if (nblocks > 0) m1(acc_s[0], 0);
 
   auto iter = [&](int j, auto par_tag) {
-    load_k((j + 2) * BKV);
-    load_v((j + 1) * BKV);
-    const int kv0 = j * BKV;
+    load_k(kv_lo + (j + 2) * BKV);
+    load_v(kv_lo + (j + 1) * BKV);
+    const int kv0 = kv_lo + j * BKV;
     // A block past the wave's last query contributes nothing, and neither
     // does any later one, whose scores S(j+1) the skipped body would compute.
     if (qw < a.s && !(CAUSAL && kv0 > qw + 31)) {
@@ -607,7 +629,27 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
     if (j + 1 < nblocks) iter(j + 1, ic<1>{});
   }
 
-  if (my_q < a.s) {
+  if constexpr (SPLIT) {
+    // This key range's unnormalised output, running max and row sum (an
+    // empty range leaves 0, -inf, 0); the combine kernel merges the ranges.
+    if (my_q < a.s) {
+      const int64_t row = (static_cast<int64_t>(sp) * a.bh + bh) * a.s + my_q;
+      float* op = a.o_part + row * D;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d = dt * 32 + 8 * g4 + 4 * h;
+          float4 v;
+          v.x = acc_o[dt][g4 * 4 + 0];
+          v.y = acc_o[dt][g4 * 4 + 1];
+          v.z = acc_o[dt][g4 * 4 + 2];
+          v.w = acc_o[dt][g4 * 4 + 3];
+          *reinterpret_cast<float4*>(op + d) = v;
+        }
+      if (h == 0) *reinterpret_cast<float2*>(a.ml_part + row * 2) = make_float2(m_run, l_run);
+    }
+  } else if (my_q < a.s) {
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
@@ -620,6 +662,32 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
         *reinterpret_cast<bf16x4*>(O + static_cast<int64_t>(my_q) * D + d) = out;
       }
   }
+}
+
+// Merges the key ranges of hw variant 3, one wave per query row (two of
+// the 128 output columns per lane): with M the largest running max,
+// O = sum_r 2^(m_r - M) O_r / sum_r 2^(m_r - M) l_r.
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ o_part,
+                                                           const float* __restrict__ ml_part,
+                                                           bf16* __restrict__ o, int nsplit,
+                                                           int64_t rows) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  float mx = -INFINITY;
+  for (int r = 0; r < nsplit; ++r) mx = fmaxf(mx, ml_part[(r * rows + row) * 2]);
+  float l = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int r = 0; r < nsplit; ++r) {
+    const float2 ml = *reinterpret_cast<const float2*>(ml_part + (r * rows + row) * 2);
+    const float w = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
+    const float2 v = *reinterpret_cast<const float2*>(o_part + (r * rows + row) * D + 2 * lane);
+    l += w * ml.y;
+    o0 += w * v.x;
+    o1 += w * v.y;
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  bf16 out[2] = {static_cast<bf16>(o0 * inv), static_cast<bf16>(o1 * inv)};
+  *reinterpret_cast<uint32_t*>(o + row * D + 2 * lane) = pack2(out[0], out[1]);
 }
 
 // ---------------------------------------------------------------------------
@@ -641,7 +709,40 @@ struct AttnTiles {
 };
 
 AttnTiles attn_tiles(const Call& c) {
+  if (c.variant == 3) return {2 * c.tile(0), c.tile(1), 1};
   return {4 * c.tile(0), c.tile(1), c.variant == 1 ? 2 : 1};
+}
+
+// hw variant 3 splits the key range over workgroups and merges the partial
+// softmax states in a second kernel; it is offered for up to this many query
+// rows (batch * heads * s), where the other variants cannot fill the GPU and
+// its workspace (nsplit * rows * 520 bytes) stays below 136 MB.
+constexpr int64_t kSplitMaxRows = 16384;
+constexpr int kMaxSplits = 16;
+
+int check_split_tiles(const Call& c, int64_t rows, std::string* why) {
+  const int tm = c.tile(0), TN = c.tile(1), ns = c.tile(2);
+  if (!(tm == 1 || tm == 2 || tm == 4)) {
+    *why = "TILES_IN_BLOCK_M (pairs of waves) must be 1, 2 or 4";
+    return AXON_EINVAL;
+  }
+  if (!(TN == 1 || TN == 2)) {
+    *why = "TILES_IN_BLOCK_N (key block / 32) must be 1 or 2";
+    return AXON_EINVAL;
+  }
+  if (!is_pow2_in(ns, 1, kMaxSplits)) {
+    *why = "TILES_IN_BLOCK_K (key-range splits) must be a power of two in [1, 16]";
+    return AXON_EINVAL;
+  }
+  if (c.tile(3) != 1) {
+    *why = "TILES_IN_BLOCK_P is unused and must be 1";
+    return AXON_EINVAL;
+  }
+  if (rows > kSplitMaxRows) {
+    *why = "split key ranges serve at most 16384 query rows (batch * heads * s)";
+    return AXON_EINVAL;
+  }
+  return AXON_OK;
 }
 
 int check_tiles(const Call& c, std::string* why) {
@@ -683,6 +784,7 @@ int check_causal(const Call& c, std::string* why) {
     *why = "dimension out of range";
     return AXON_EINVAL;
   }
+  if (c.variant == 3) return check_split_tiles(c, c.dim(0) * c.dim(1) * c.dim(2), why);
   return check_tiles(c, why);
 }
 
@@ -709,32 +811,64 @@ int check_nki(const Call& c, std::string* why) {
     *why = "s must be a multiple of 8 (16-byte rows of k_t)";
     return AXON_EINVAL;
   }
+  if (c.variant == 3) return check_split_tiles(c, c.dim(0), why);
   return check_tiles(c, why);
 }
 
-int manifest_attn(int variant, const int64_t* dims, int, Constraint* out, int cap, int64_t s) {
-  (void)dims;
+int manifest_attn(int variant, Constraint* out, int cap, int64_t s, int64_t rows) {
   if (cap < 4) return 0;
   const int64_t sq = s > 0 ? s : 1;
-  const int64_t kmax = variant == 0 ? 128 : 64;  // key block (variants 1, 2: at most 64)
-  out[0] = {"TILES_IN_BLOCK_M", variant == 1 ? 1 : 2, 1, false};
+  const int64_t kmax = variant == 0 ? 128 : 64;  // key block (variants 1-3: at most 64)
+  out[0] = {"TILES_IN_BLOCK_M", variant == 1 ? 1 : (variant == 3 ? 4 : 2), 1, false};
   out[1] = {"TILES_IN_BLOCK_N", sq < kmax ? (sq < 32 ? 32 : sq) : kmax, 32, false};
-  out[2] = {"TILES_IN_BLOCK_K", 1, 1, false};
+  out[2] = {"TILES_IN_BLOCK_K", variant == 3 ? (rows <= kSplitMaxRows ? kMaxSplits : 0) : 1, 1, false};
   out[3] = {"TILES_IN_BLOCK_P", 1, 1, false};
   return 4;
 }
 
 int manifest_causal(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   (void)dt;
-  return manifest_attn(v, dims, dt, out, cap, dims[2]);
+  return manifest_attn(v, out, cap, dims[2], dims[0] * dims[1] * dims[2]);
 }
 
 int manifest_nki(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   (void)dt;
-  return manifest_attn(v, dims, dt, out, cap, dims[0]);
+  return manifest_attn(v, out, cap, dims[0], dims[0]);
 }
 
-size_t no_workspace(const Call&) { return 0; }
+// Split key ranges: keys per range (a multiple of the key block) and the
+// number of non-empty ranges.
+struct SplitPlan {
+  int kv_split, nsplit;
+};
+
+SplitPlan split_plan(int64_t s, int TN, int ns) {
+  const int64_t bkv = 32 * TN;
+  const int64_t per = ((s + ns - 1) / ns + bkv - 1) / bkv * bkv;
+  const int64_t used = per > 0 ? (s + per - 1) / per : 0;
+  return {static_cast<int>(per > 0 ? per : bkv), static_cast<int>(used)};
+}
+
+// Workspace of hw variant 3: [nsplit][rows][D] fp32 outputs, then
+// [nsplit][rows][2] fp32 (max, sum), at a 256-byte boundary.
+size_t split_ws_bytes(int64_t rows, int nsplit, size_t* ml_off) {
+  const size_t o = static_cast<size_t>(nsplit) * rows * D * sizeof(float);
+  *ml_off = (o + 255) / 256 * 256;
+  return *ml_off + static_cast<size_t>(nsplit) * rows * 2 * sizeof(float);
+}
+
+size_t workspace_attn(const Call& c, int64_t rows, int64_t s) {
+  if (c.variant != 3) return 0;
+  const SplitPlan p = split_plan(s, c.tile(1), c.tile(2));
+  size_t ml_off;
+  return split_ws_bytes(rows, p.nsplit, &ml_off);
+}
+
+size_t workspace_causal(const Call& c) {
+  return workspace_attn(c, c.dim(0) * c.dim(1) * c.dim(2), c.dim(2));
+}
+
+size_t workspace_nki(const Call& c) { return workspace_attn(c, c.dim(0), c.dim(0)); }
 
 void outputs_causal(const int64_t* dims, const int32_t*, OutDesc* out) {
   out[0] = {4, {dims[0], dims[1], dims[2], dims[3]}, AXON_BF16};
@@ -759,23 +893,39 @@ int launch_t(const AttnArgs& a, hipStream_t st) {
   return launch_status("attn_kernel");
 }
 
-template <int W, int TN, bool CAUSAL, bool KT>
+template <int W, int TN, bool CAUSAL, bool KT, bool SPLIT = false>
 int launch_sp(const AttnArgs& a, hipStream_t st) {
   const size_t lds = attn_lds(TN);
-  auto fn = attn_sp_kernel<W, TN, CAUSAL, KT>;
+  auto fn = attn_sp_kernel<W, TN, CAUSAL, KT, SPLIT>;
   static std::atomic<bool> configured{false};
   if (!configured.load(std::memory_order_acquire)) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                               static_cast<int>(lds));
     configured.store(true, std::memory_order_release);
   }
-  const unsigned blocks = static_cast<unsigned>(a.qblocks) * static_cast<unsigned>(a.bh);
+  const unsigned blocks = static_cast<unsigned>(a.qblocks) * static_cast<unsigned>(a.bh) *
+                         static_cast<unsigned>(SPLIT ? a.nsplit : 1);
   hipLaunchKernelGGL(fn, dim3(blocks), dim3(W * 64), lds, st, a);
-  return launch_status("attn_sp_kernel");
+  int rc = launch_status("attn_sp_kernel");
+  if (!SPLIT || rc != AXON_OK) return rc;
+  const int64_t rows = static_cast<int64_t>(a.bh) * a.s;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, st,
+                     a.o_part, a.ml_part, a.o, a.nsplit, rows);
+  return launch_status("attn_combine_kernel");
 }
 
 template <bool CAUSAL, bool KT>
 int dispatch(int W, int TN, int QT, const AttnArgs& a, hipStream_t st, int variant) {
+  if (variant == 3) {
+    if (W == 2 && TN == 1) return launch_sp<2, 1, CAUSAL, KT, true>(a, st);
+    if (W == 2 && TN == 2) return launch_sp<2, 2, CAUSAL, KT, true>(a, st);
+    if (W == 4 && TN == 1) return launch_sp<4, 1, CAUSAL, KT, true>(a, st);
+    if (W == 4 && TN == 2) return launch_sp<4, 2, CAUSAL, KT, true>(a, st);
+    if (W == 8 && TN == 1) return launch_sp<8, 1, CAUSAL, KT, true>(a, st);
+    if (W == 8 && TN == 2) return launch_sp<8, 2, CAUSAL, KT, true>(a, st);
+    set_error("no split-range attention instantiation for this tile");
+    return AXON_EINVAL;
+  }
   if (variant == 2) {
     if (W == 4 && TN == 1) return launch_sp<4, 1, CAUSAL, KT>(a, st);
     if (W == 4 && TN == 2) return launch_sp<4, 2, CAUSAL, KT>(a, st);
@@ -794,8 +944,8 @@ int dispatch(int W, int TN, int QT, const AttnArgs& a, hipStream_t st, int varia
   return AXON_EINVAL;
 }
 
-int launch_common(const Call& c, const void* const* in, void* const* out, hipStream_t st, int64_t bh,
-                  int64_t s, bool causal) {
+int launch_common(const Call& c, const void* const* in, void* const* out, void* ws, hipStream_t st,
+                  int64_t bh, int64_t s, bool causal) {
   if (bh == 0 || s == 0) return AXON_OK;
   for (int i = 0; i < 3; ++i)
     if (!aligned16(in[i])) {
@@ -822,6 +972,22 @@ int launch_common(const Call& c, const void* const* in, void* const* out, hipStr
   }
   // Deal heads to XCDs (workgroup b runs on XCD b % 8) when they split evenly.
   a.xcd_heads = a.bh % kXcds == 0 ? a.bh / kXcds : 0;
+  a.nsplit = 1;
+  a.kv_split = a.s;
+  a.o_part = a.ml_part = nullptr;
+  if (c.variant == 3) {
+    const SplitPlan p = split_plan(s, TN, c.tile(2));
+    size_t ml_off;
+    split_ws_bytes(bh * s, p.nsplit, &ml_off);
+    a.nsplit = p.nsplit;
+    a.kv_split = p.kv_split;
+    a.o_part = static_cast<float*>(ws);
+    a.ml_part = reinterpret_cast<float*>(static_cast<char*>(ws) + ml_off);
+    if (static_cast<int64_t>(a.qblocks) * a.bh * a.nsplit > (1LL << 31) - 1) {
+      set_error("grid too large");
+      return AXON_EINVAL;
+    }
+  }
   if (causal) {
     a.scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
     return dispatch<true, false>(W, TN, QT, a, st, c.variant);
@@ -830,12 +996,12 @@ int launch_common(const Call& c, const void* const* in, void* const* out, hipStr
   return dispatch<false, true>(W, TN, QT, a, st, c.variant);
 }
 
-int launch_causal(const Call& c, const void* const* in, void* const* out, void*, hipStream_t st) {
-  return launch_common(c, in, out, st, c.dim(0) * c.dim(1), c.dim(2), true);
+int launch_causal(const Call& c, const void* const* in, void* const* out, void* ws, hipStream_t st) {
+  return launch_common(c, in, out, ws, st, c.dim(0) * c.dim(1), c.dim(2), true);
 }
 
-int launch_nki(const Call& c, const void* const* in, void* const* out, void*, hipStream_t st) {
-  return launch_common(c, in, out, st, 1, c.dim(0), false);
+int launch_nki(const Call& c, const void* const* in, void* const* out, void* ws, hipStream_t st) {
+  return launch_common(c, in, out, ws, st, 1, c.dim(0), false);
 }
 
 const char* summary_attn(int variant) {
@@ -847,21 +1013,27 @@ const char* summary_attn(int variant) {
              : variant == 1
                    ? "flash attention as hw variant 0 with two 32-query tiles per wave (4 waves, one "
                      "per SIMD): every K and V^T fragment read from LDS feeds two MFMAs"
-                   : "flash attention as hw variant 0, software-pipelined: K staged a block ahead of "
-                     "V so each wave runs the next block's QK MFMAs under its softmax of this block";
+                   : variant == 2
+                         ? "flash attention as hw variant 0, software-pipelined: K staged a block ahead "
+                           "of V so each wave runs the next block's QK MFMAs under its softmax of this "
+                           "block"
+                         : "flash attention as hw variant 2 over split key ranges (2, 4 or 8 waves of "
+                           "32 queries per workgroup): each range writes its unnormalised output, "
+                           "running max and row sum, and a second kernel merges the ranges; fills the "
+                           "GPU when batch * heads * s is small";
 }
 
 }  // namespace
 
 const Family* family_attention_causal() {
-  static const Family f = {"attention_causal", 3, 3, 1, 4, kTileArgs, 4, summary_attn,
-                           manifest_causal, check_causal, no_workspace, outputs_causal, launch_causal};
+  static const Family f = {"attention_causal", 4, 3, 1, 4, kTileArgs, 4, summary_attn,
+                           manifest_causal, check_causal, workspace_causal, outputs_causal, launch_causal};
   return &f;
 }
 
 const Family* family_attention_nkilib() {
-  static const Family f = {"attention_nkilib", 3, 3, 1, 2, kTileArgs, 4, summary_attn, manifest_nki,
-                           check_nki, no_workspace, outputs_nki, launch_nki};
+  static const Family f = {"attention_nkilib", 4, 3, 1, 2, kTileArgs, 4, summary_attn, manifest_nki,
+                           check_nki, workspace_nki, outputs_nki, launch_nki};
   return &f;
 }
 

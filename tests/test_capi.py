@@ -108,7 +108,10 @@ def test_legal_tiles_are_a_subset_of_the_manifest():
             cons = hip.manifest(name, v, dims, dt[0])
             legal = [t for t in product(spec.tile_options, repeat=len(spec.tile_args))
                      if hip.check(name, v, t, dims, dt)[0] == hip.AXON_OK]
-            assert legal, (name, v)
+            # A variant that does not serve this shape says so in its manifest
+            # (an extent of 0 admits nothing), e.g. attention's split key
+            # ranges above 16384 query rows.
+            assert legal or any(c.extent == 0 for c in cons), (name, v)
             for t in legal:
                 assert rejection_reason(spec.tile_args, t, cons) is None, (name, v, t)
 
@@ -143,10 +146,10 @@ def test_manifest_admits_only_legal_tiles():
                 tuples = list(product(spec.tile_options, repeat=len(spec.tile_args)))
                 admitted = [t for t in tuples if rejection_reason(spec.tile_args, t, cons) is None]
                 if not admitted:
-                    # A variant without an instantiation for this dtype admits
-                    # nothing, and the library agrees.
-                    assert all(hip.check(name, v, t, dvals, codes)[0] == hip.AXON_EDTYPE
-                               for t in tuples[:8]), (name, cid, v)
+                    # A variant without an instantiation for this dtype or
+                    # shape admits nothing, and the library agrees.
+                    assert all(hip.check(name, v, t, dvals, codes)[0] in (hip.AXON_EDTYPE, hip.AXON_EINVAL)
+                               for t in tuples), (name, cid, v)
                     continue
                 served += 1
                 for t in admitted:

@@ -31,3 +31,17 @@ def test_attention_causal_config():
 @pytest.mark.parametrize("sizes", [(1024, 128), (2048, 128), (200, 128)])
 def test_attention_nkilib(sizes):
     assert check_parity("attention_nkilib", sizes, rtol=1e-2, atol=1e-2, budget=5)
+
+
+@pytest.mark.parametrize("name,sizes", [("attention_nkilib", (1024, 128)), ("attention_nkilib", (8192, 128)),
+                                        ("attention_causal", (1, 2, 1000, 128)),
+                                        ("attention_causal", (2, 2, 33, 128))])
+def test_attention_split_key_ranges(name, sizes):
+    """hw variant 3 (split key ranges merged by a second kernel): every
+    split count and wave count, including ranges left empty by the causal
+    mask or by a short sequence."""
+    for ns in (1, 2, 4, 8, 16):
+        for tm in (1, 2, 4):
+            for tn in (1, 2):
+                print(f"{name} {sizes} v3 tiles {(tm, tn, ns, 1)}", flush=True)
+                assert check_parity(name, sizes, rtol=1e-2, atol=1e-2, variants=[3], tiles=(tm, tn, ns, 1)) == 1
