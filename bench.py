@@ -48,6 +48,7 @@ import math
 import os
 import sys
 import time
+import warnings
 from pathlib import Path
 
 import numpy as np
@@ -158,9 +159,13 @@ def timed_launches(launch, n_sets: int, steps: int, warmup: int, settle_ms: floa
             chunk *= 2
     settled = w0.elapsed_time(w1)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(steps):
-            launch((done + i) % n_sets)
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        with torch.cuda.graph(graph):
+            for i in range(steps):
+                launch((done + i) % n_sets)
+    if any("empty" in str(w.message) for w in caught):
+        raise RuntimeError("the timed launches were not captured (launched off the capture stream)")
     # The capture left the GPU idle for a moment: a short eager burst
     # (2 ms of launches) brings the clocks back before the replay.
     with torch.cuda.stream(stream):

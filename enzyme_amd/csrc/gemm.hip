@@ -1046,6 +1046,28 @@ __global__ __launch_bounds__(256) void qkv_split_w_kernel(const float* __restric
   store_vec(b + 2 * kn + i, lo);
 }
 
+// A operand of the fp32 matmul: x [m, k] fp32 -> [m, 3k] bf16 rows
+// [hi(x) | lo(x) | hi(x)] (paired with w as [hi; hi; lo], as in qkv_cte).
+// Every thread converts 8 consecutive elements of one row (k % 8 == 0).
+__global__ __launch_bounds__(256) void split_rows_hilo_kernel(const float* __restrict__ x,
+                                                             bf16* __restrict__ a, int64_t mk, int k) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  if (i >= mk) return;
+  const int64_t row = i / k, col = i - row * k;
+  const Vec<float> v0 = load_vec_nt(x + i), v1 = load_vec_nt(x + i + 4);
+  Vec<bf16> hi, lo;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float f = e < 4 ? v0.v[e] : v1.v[e - 4];
+    hi.v[e] = static_cast<bf16>(f);
+    lo.v[e] = static_cast<bf16>(f - static_cast<float>(hi.v[e]));
+  }
+  bf16* arow = a + row * 3 * k;
+  store_vec(arow + col, hi);
+  store_vec(arow + k + col, lo);
+  store_vec(arow + 2 * k + col, hi);
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -1328,8 +1350,34 @@ int manifest_mm(int, const int64_t* dims, int, Constraint* out, int cap) {
 // that needs whole 64-deep K steps.
 constexpr int kDmaVariant = 2;
 
+// fp32 inputs (hw variants 0 and 1): a prep pass splits x into bf16 rows
+// [hi | lo | hi] and w into planes [hi; hi; lo], and the bf16 GEMM over
+// K' = 3k sums hi*hi + lo*hi + hi*lo with an fp32 output, leaving out only
+// the lo*lo term (about 2^-16 relative).
+int plain_kp(int64_t k, int dtype) { return static_cast<int>(dtype == AXON_F32 ? 3 * k : k); }
+
 int check_plain(const Call& c, std::string* why) {
-  const int rc = check_mm<kPlain>(c, why);
+  if (c.n_tiles != 3 || c.n_dims != 3 || c.n_dtypes != 2) {
+    *why = "expected 3 tiles, 3 dims (m, n, k) and 2 dtypes";
+    return AXON_EARG;
+  }
+  const int dt = c.dtype(0);
+  if ((dt != AXON_BF16 && dt != AXON_F32) || c.dtype(1) != dt) {
+    *why = "x and w must both be bf16 or both fp32";
+    return AXON_EDTYPE;
+  }
+  if (dt == AXON_F32) {
+    if (c.variant == kDmaVariant) {
+      *why = "hw variant 2 has no fp32 instantiation; fp32 inputs use hw variants 0 and 1";
+      return AXON_EDTYPE;
+    }
+    if (c.dim(2) % 8 != 0 || c.dim(2) > (1 << 28)) {
+      *why = "fp32 inputs need k % 8 == 0 (16-byte groups of one row) and k < 2^28";
+      return AXON_EINVAL;
+    }
+  }
+  const int rc = check_gemm_shape(c.dim(0), c.dim(1), plain_kp(c.dim(2), dt), c.tile(0), c.tile(1),
+                                  c.tile(2), why);
   if (rc != AXON_OK) return rc;
   if (c.variant == kDmaVariant && c.dim(2) % BK != 0) {
     *why = "hw variant 2 loads whole 64-deep K steps: k must be a multiple of 64";
@@ -1339,10 +1387,64 @@ int check_plain(const Call& c, std::string* why) {
 }
 
 int manifest_plain(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
-  const int n = manifest_mm(v, dims, dt, out, cap);
-  if (v == kDmaVariant && dims[2] % BK != 0)
+  const int64_t mnk[3] = {dims[0], dims[1], dt == AXON_F32 ? 3 * dims[2] : dims[2]};
+  const int n = manifest_mm(v, mnk, dt, out, cap);
+  if (v == kDmaVariant && (dims[2] % BK != 0 || dt == AXON_F32))
     for (int i = 0; i < n; ++i) out[i].extent = 0;  // admits no tile
   return n;
+}
+
+struct PlainLayout {
+  Plan p;
+  int kp;
+  size_t a, b, data, total;  // byte offsets: A' [m][K'], B' [K'][n] (fp32 only), split-K data
+};
+
+PlainLayout plain_layout(const Call& c) {
+  const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1));
+  PlainLayout L;
+  L.kp = plain_kp(c.dim(2), c.dtype(0));
+  L.p = plan_of(m, n, L.kp, c.tile(0), c.tile(1), c.tile(2));
+  L.a = L.b = L.data = 0;
+  if (c.dtype(0) == AXON_F32) {
+    L.b = align256(static_cast<size_t>(m) * L.kp * sizeof(bf16));
+    L.data = L.b + align256(static_cast<size_t>(L.kp) * n * sizeof(bf16));
+  }
+  L.total = L.data + data_bytes(L.p, m, n, 1);
+  return L;
+}
+
+size_t workspace_plain(const Call& c) { return plain_layout(c).total; }
+
+template <int EPI>
+int launch_mm(const Call& c, const void* const* in, void* const* out, void* ws, hipStream_t st);
+
+int launch_plain(const Call& c, const void* const* in, void* const* out, void* ws, hipStream_t st) {
+  if (c.dtype(0) != AXON_F32) return launch_mm<kPlain>(c, in, out, ws, st);
+  const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1)), k = static_cast<int>(c.dim(2));
+  if (m == 0 || n == 0) return AXON_OK;
+  if (!aligned16(in[0]) || !aligned16(in[1]) || !aligned16(out[0])) {
+    set_error("GEMM buffers must be 16-byte aligned");
+    return AXON_EARG;
+  }
+  const PlainLayout L = plain_layout(c);
+  char* base = static_cast<char*>(ws);
+  bf16* a = reinterpret_cast<bf16*>(base + L.a);
+  bf16* b = reinterpret_cast<bf16*>(base + L.b);
+  const int64_t mk = static_cast<int64_t>(m) * k, kn = static_cast<int64_t>(k) * n;
+  if (mk > 0) {
+    hipLaunchKernelGGL(split_rows_hilo_kernel, dim3(static_cast<unsigned>((mk / 8 + 255) / 256)), dim3(256), 0,
+                       st, static_cast<const float*>(in[0]), a, mk, k);
+    int rc = launch_status("split_rows_hilo_kernel");
+    if (rc != AXON_OK) return rc;
+    hipLaunchKernelGGL(qkv_split_w_kernel, dim3(static_cast<unsigned>((kn / 8 + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const float*>(in[1]), b, kn);
+    rc = launch_status("qkv_split_w_kernel");
+    if (rc != AXON_OK) return rc;
+  }
+  GemmArgs g = make_args(a, b, nullptr, out[0], m, n, L.kp, L.p, base + L.data, 1, 1e-6f);
+  g.c_f32 = 1;
+  return dispatch<kPlain, false>(L.p.BM, L.p.BN, g, st, c.variant);
 }
 
 template <int EPI>
@@ -1351,8 +1453,9 @@ size_t workspace_mm(const Call& c) {
                         static_cast<int>(c.dim(2)), c.tile(0), c.tile(1), c.tile(2), 1);
 }
 
-void outputs_mm(const int64_t* dims, const int32_t*, OutDesc* out) {
-  out[0] = {2, {dims[0], dims[1]}, AXON_BF16};
+// fp32 output for fp32 inputs (only the plain matmul families accept them).
+void outputs_mm(const int64_t* dims, const int32_t* dtypes, OutDesc* out) {
+  out[0] = {2, {dims[0], dims[1]}, dtypes[0] == AXON_F32 ? AXON_F32 : AXON_BF16};
 }
 
 template <int EPI>
@@ -2026,7 +2129,7 @@ const char* summary_attn_qkv(int variant) {
   const Family* fn_name() {                                                                    \
     static const Family f = {spec_name,     3,          2,              1,           3,        \
                              kTileArgs3,    3,          summary_mm,     manifest_plain, check_plain, \
-                             workspace_mm<kPlain>, outputs_mm, launch_mm<kPlain>};               \
+                             workspace_plain, outputs_mm, launch_plain};                         \
     return &f;                                                                                 \
   }
 

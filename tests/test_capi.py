@@ -135,6 +135,8 @@ def test_manifest_admits_only_legal_tiles():
             continue
         spec = load_spec(name)
         for cid, case in per_case.items():
+            if cid.startswith("_"):
+                continue
             dims = dict(zip(spec.dim_vars, case["sizes"]))
             small = tuple(min(v, 8) for v in case["sizes"])
             _, _, ins = spec_inputs(name, small, dtype=case.get("dtype"))

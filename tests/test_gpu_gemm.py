@@ -7,6 +7,10 @@ both hw variants (one or several K steps of loads in flight), at the
 reference's case shapes, the BASELINE shapes (1024 x 512 x 16384) and ragged
 shapes (m not a multiple of the tile).
 
+fp32 matmul (hi/lo bf16 planes over K' = 3k, fp32 output) is held to the
+reference's fp32 tolerance rtol = atol = 1e-3 at its ck_16k_l2 shape
+(1024 x 1024 x 16384) and at ragged shapes.
+
 silu_mlp with the spec's unscaled N(0, 1) inputs has outputs up to ~1e5, so
 an absolute 1e-2 is below fp32 summation-order noise there; that case is
 held to rtol 1e-2 with atol 1e-3 * max|ref| (a normwise bound), and a scaled
@@ -93,3 +97,14 @@ def test_silu_mlp_scaled_elementwise():
         torch.cuda.synchronize()
         torch.testing.assert_close(ln.outputs[0].float().cpu(), ref, rtol=1e-2, atol=1e-2,
                                    msg=lambda s, t=tiles: f"tiles {t}: {s}")
+
+
+@pytest.mark.parametrize("sizes", [(1024, 1024, 16384), (100, 72, 200), (33, 520, 1032), (1, 8, 8)])
+def test_matmul_fp32(sizes):
+    """fp32 x and w through hw variants 0 and 1 (variant 2 has no fp32
+    instantiation and is refused)."""
+    print(f"matmul fp32 {sizes}", flush=True)
+    assert check_parity("matmul", sizes, rtol=1e-3, atol=1e-3, dtype="float32", variants=[0, 1],
+                        budget=4 if sizes[2] > 10000 else 8)
+    codes = [hip.AXON_F32, hip.AXON_F32]
+    assert hip.check("matmul", 2, (1, 1, 1), sizes, codes)[0] == hip.AXON_EDTYPE
