@@ -330,6 +330,8 @@ def main(argv=None) -> int:
                     help="minimum device time of untimed launches before each timed region")
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline timing")
+    ap.add_argument("--config", action="append", default=[], metavar="SPEC",
+                    help="measure only these workload rows (spec names); the headline row is the first")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(
@@ -344,8 +346,14 @@ def main(argv=None) -> int:
         print("bench.py needs a visible GPU", file=sys.stderr)
         return 2
 
+    configs = CONFIGS[:1] if args.headline_only else CONFIGS
+    if args.config:
+        configs = [c for c in CONFIGS if c["spec"] in args.config]
+        if not configs:
+            print(f"bench.py: no workload named {args.config}", file=sys.stderr)
+            return 2
     rows = []
-    for cfg in CONFIGS[:1] if args.headline_only else CONFIGS:
+    for cfg in configs:
         us, settled, launches, outs, host = measure(cfg, args.steps, args.warmup, args.settle_ms)
         row = {"spec": cfg["spec"], "label": cfg["label"], "sizes": list(cfg["sizes"]),
                "tiles": list(cfg["tiles"]), "hw_variant": cfg["variant"], "us_per_launch": round(us, 3),
@@ -373,7 +381,7 @@ def main(argv=None) -> int:
               f"(max abs err {row['max_abs_err']:.3g}), settle {settled:.1f} ms / {launches} launches",
               file=sys.stderr, flush=True)
 
-    head, hrow = CONFIGS[0], rows[0]
+    head, hrow = configs[0], rows[0]
     line = {
         "metric": METRIC,
         "value": hrow["achieved"],
@@ -398,7 +406,9 @@ def main(argv=None) -> int:
         "settle_launches": hrow["settle_launches"],
         "allclose": hrow["allclose"],
         "roofline": {k: hrow[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
-        "copy_ceiling": {
+    }
+    if "copy_us" in hrow:
+        line["copy_ceiling"] = {
             "us": hrow["copy_us"],
             "achieved": round(head["work"] / (hrow["copy_us"] * 1e-6) / 1e9, 2),
             "unit": "GB/s",
@@ -406,8 +416,7 @@ def main(argv=None) -> int:
             "what": "fastest of four plain 16-byte-vector copy launch shapes reading and writing half "
                     "the headline's algorithmic bytes each, same buffer rotation: the HBM rate a "
                     "streaming kernel of this size reaches here",
-        },
-    }
+        }
     if "cpu_ms" in hrow:
         line["cpu_baseline"] = {
             "value": round(head["work"] / (hrow["cpu_ms"] * 1e-3) / 1e9, 3),

@@ -15,7 +15,8 @@
 // index space (q first), so one launch covers both tensors; x is read once
 // and written once.
 // Tile arguments: TILES_IN_BLOCK_M = W (waves per workgroup),
-//                 TILES_IN_BLOCK_N = H (head rows per thread).
+//                 TILES_IN_BLOCK_N = H (head rows per thread; hw variant 1:
+//                 tokens per workgroup).
 #include "common.hpp"
 #include "registry.hpp"
 
@@ -94,6 +95,117 @@ __global__ __launch_bounds__(1024) void rope_tok_kernel(
   }
 }
 
+// hw variant 1 (token-aligned workgroups): workgroup b owns tokens
+// [b * TPB, (b + 1) * TPB) whole. It stages their cos/sin rows in LDS with one
+// 16-byte load per vector, so each row leaves HBM once and is read by one
+// XCD only (hw variant 0's workgroups straddle tokens, and a token's rows are
+// fetched again by the neighbouring workgroup on another XCD: 52.9 MB read
+// against 46.1 MB at the Llama-3-8B shape). Slot i of the workgroup is (token
+// i / (nh * J), head, pair slice j), j fastest, as in variant 0 with H = 1; a
+// thread walks its slots in chunks of U whose x loads are all issued before
+// any arithmetic. The first chunk's loads are issued before the LDS barrier.
+constexpr int kRopeU = 4;
+
+template <typename T>
+__global__ __launch_bounds__(1024) void rope_tokgroup_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const float* __restrict__ cs,
+    const float* __restrict__ sn, T* __restrict__ qo, T* __restrict__ ko, int64_t tokens,
+    int64_t s, int hq, int hkv, int d, int TPB) {
+  constexpr int E = EPV<T>::value;
+  extern __shared__ __align__(16) float rows[];  // [TPB][2][d]: cos row, sin row
+  const int half = d >> 1;
+  const int J = half / E;
+  const int nh = hq + hkv;
+  const int per_token = nh * J;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TPB;
+  const int ntok = static_cast<int>(min<int64_t>(TPB, tokens - t0));
+  const int total = ntok * per_token;
+  const int nt = blockDim.x;
+
+  Vec<T> lo[kRopeU], hi[kRopeU];
+  int tt[kRopeU], jj[kRopeU];
+  T* dst[kRopeU];
+  bool live[kRopeU];
+  // Issue the x loads of the chunk starting at slot `base` (slots past the
+  // end re-read the workgroup's first slot and are not stored).
+  auto load_chunk = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < kRopeU; ++u) {
+      const int slot0 = base + u * nt;
+      live[u] = slot0 < total;
+      const int slot = live[u] ? slot0 : 0;
+      tt[u] = slot / per_token;
+      const int rem = slot - tt[u] * per_token;
+      const int h = rem / J;
+      jj[u] = rem - h * J;
+      const int64_t t = t0 + tt[u];
+      const T* src = h < hq ? q + (t * hq + h) * d : k + (t * hkv + (h - hq)) * d;
+      dst[u] = h < hq ? qo + (t * hq + h) * d : ko + (t * hkv + (h - hq)) * d;
+      lo[u] = load_vec_nt(src + jj[u] * E);
+      hi[u] = load_vec_nt(src + half + jj[u] * E);
+    }
+  };
+
+  // cos/sin rows of this workgroup's tokens: 2 * d / 4 vectors per token.
+  const int vrow = d / 4;
+  const int nvec = ntok * 2 * vrow;
+  // Branch-free: a vector index past the end re-copies vector 0 (the same
+  // value thread 0 writes there), so the loads stay ahead of the x loads and
+  // in flight together.
+  const int p0 = static_cast<int>(t0 % s);  // position of the workgroup's first token
+  const int si = static_cast<int>(s);
+  auto row_vec = [&](int i) -> const float4* {
+    const int tok = i / (2 * vrow), rem = i - tok * 2 * vrow;
+    const int which = rem / vrow, c = rem - which * vrow;
+    int pos = p0 + tok;
+    while (pos >= si) pos -= si;
+    return reinterpret_cast<const float4*>((which ? sn : cs) + static_cast<int64_t>(pos) * d + c * 4);
+  };
+  const int i0 = threadIdx.x, i1 = threadIdx.x + nt;
+  const int c0 = i0 < nvec ? i0 : 0, c1 = i1 < nvec ? i1 : 0;
+  const float4 cv0 = *row_vec(c0), cv1 = *row_vec(c1);
+  load_chunk(threadIdx.x);
+  __builtin_amdgcn_sched_barrier(0);
+  reinterpret_cast<float4*>(rows)[c0] = cv0;
+  reinterpret_cast<float4*>(rows)[c1] = cv1;
+  constexpr int kR = 2;
+  for (int i = threadIdx.x + kR * nt; i < nvec; i += nt)  // more than kR vectors per thread
+    reinterpret_cast<float4*>(rows)[i] = *row_vec(i);
+  __syncthreads();
+
+  for (int base = threadIdx.x;;) {
+#pragma unroll
+    for (int u = 0; u < kRopeU; ++u) {
+      const float* crow = rows + tt[u] * 2 * d;
+      const float* srow = crow + d;
+      Vec<T> olo, ohi;
+#pragma unroll
+      for (int e0 = 0; e0 < E; e0 += 4) {
+        const float4 c_lo = *reinterpret_cast<const float4*>(crow + jj[u] * E + e0);
+        const float4 c_hi = *reinterpret_cast<const float4*>(crow + half + jj[u] * E + e0);
+        const float4 s_lo = *reinterpret_cast<const float4*>(srow + jj[u] * E + e0);
+        const float4 s_hi = *reinterpret_cast<const float4*>(srow + half + jj[u] * E + e0);
+        const float cl[4] = {c_lo.x, c_lo.y, c_lo.z, c_lo.w}, ch[4] = {c_hi.x, c_hi.y, c_hi.z, c_hi.w};
+        const float sl[4] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w}, sh[4] = {s_hi.x, s_hi.y, s_hi.z, s_hi.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = to_f32(lo[u].v[e0 + e]);
+          const float b = to_f32(hi[u].v[e0 + e]);
+          olo.v[e0 + e] = from_f32<T>(a * cl[e] - b * sl[e]);
+          ohi.v[e0 + e] = from_f32<T>(b * ch[e] + a * sh[e]);
+        }
+      }
+      if (live[u]) {
+        store_vec_nt(dst[u] + jj[u] * E, olo);
+        store_vec_nt(dst[u] + half + jj[u] * E, ohi);
+      }
+    }
+    base += kRopeU * nt;
+    if (base >= total) break;
+    load_chunk(base);
+  }
+}
+
 // Element-at-a-time fallback for head dims or pointers the vector path
 // cannot take: one thread per (token, head, pair).
 template <typename T>
@@ -154,17 +266,29 @@ int check_tok(const Call& c, std::string* why) {
     return AXON_EINVAL;
   }
   if (!is_pow2_in(c.tile(1), 1, 16)) {
-    *why = "TILES_IN_BLOCK_N (heads per thread) must be a power of two in [1, 16]";
+    *why = c.variant == 1 ? "TILES_IN_BLOCK_N (tokens per workgroup) must be a power of two in [1, 16]"
+                          : "TILES_IN_BLOCK_N (heads per thread) must be a power of two in [1, 16]";
+    return AXON_EINVAL;
+  }
+  if (c.variant == 1 && static_cast<int64_t>(c.tile(1)) * 2 * c.dim(4) * 4 > 64 * 1024) {
+    *why = "TILES_IN_BLOCK_N: the tokens' cos/sin rows exceed 64 KiB of LDS";
     return AXON_EINVAL;
   }
   return AXON_OK;
 }
 
-int manifest_tok(int, const int64_t* dims, int, Constraint* out, int cap) {
+int manifest_tok(int variant, const int64_t* dims, int, Constraint* out, int cap) {
   if (cap < 2) return 0;
   const int64_t nh = dims[2] + dims[3];
   out[0] = {"TILES_IN_BLOCK_M", 16, 1, false};
-  out[1] = {"TILES_IN_BLOCK_N", nh < 16 ? (nh > 0 ? nh : 1) : 16, 1, false};
+  if (variant == 1) {
+    // Tokens per workgroup: at most 16, and their cos/sin rows within 64 KiB.
+    int64_t t = 16;
+    while (t > 1 && t * 2 * dims[4] * 4 > 64 * 1024) t >>= 1;
+    out[1] = {"TILES_IN_BLOCK_N", t, 1, false};
+  } else {
+    out[1] = {"TILES_IN_BLOCK_N", nh < 16 ? (nh > 0 ? nh : 1) : 16, 1, false};
+  }
   return 2;
 }
 
@@ -209,6 +333,19 @@ int launch_tok_t(const Call& c, const void* const* in, void* const* out, hipStre
   for (const void* p : {in[0], in[1], in[2], in[3], static_cast<const void*>(out[0]),
                         static_cast<const void*>(out[1])})
     vec = vec && aligned16(p);
+  if (vec && c.variant == 1) {
+    const int W = c.tile(0), TPB = c.tile(1);
+    const int bd = W * kWave;
+    const size_t lds = static_cast<size_t>(TPB) * 2 * d * sizeof(float);
+    if (lds > 64 * 1024) {
+      set_error("rope_llama3 v1: TILES_IN_BLOCK_N tokens of cos/sin rows exceed 64 KiB of LDS");
+      return AXON_EINVAL;
+    }
+    const int64_t blocks = (tokens + TPB - 1) / TPB;
+    hipLaunchKernelGGL(rope_tokgroup_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(bd), lds, st, q,
+                       k, cs, sn, qo, ko, tokens, s, hq, hkv, d, TPB);
+    return launch_status("rope_tokgroup_kernel");
+  }
   if (vec) {
     const int W = c.tile(0), H = c.tile(1);
     const int HG = (nh + H - 1) / H;
@@ -232,15 +369,19 @@ int launch_tok(const Call& c, const void* const* in, void* const* out, void*, hi
                                  : launch_tok_t<float>(c, in, out, st);
 }
 
-const char* summary_tok(int) {
-  return "token-major rotate-half: one thread per (token, head group, pair slice), cos/sin "
-         "slices loaded once and reused for H interleaved heads; q and k in one launch";
+const char* summary_tok(int variant) {
+  return variant == 1
+             ? "token-major rotate-half, token-aligned workgroups of TILES_IN_BLOCK_N tokens: their "
+               "cos/sin rows staged once in LDS (each row read from HBM by one XCD), slots walked in "
+               "chunks of 4 with the x loads in flight together; q and k in one launch"
+             : "token-major rotate-half: one thread per (token, head group, pair slice), cos/sin "
+               "slices loaded once and reused for H interleaved heads; q and k in one launch";
 }
 
 }  // namespace
 
 const Family* family_rope_llama3() {
-  static const Family f = {"rope_llama3", 1, 4, 2, 5, kTileArgs, 2, summary_tok, manifest_tok,
+  static const Family f = {"rope_llama3", 2, 4, 2, 5, kTileArgs, 2, summary_tok, manifest_tok,
                            check_tok, no_workspace, outputs_tok, launch_tok};
   return &f;
 }

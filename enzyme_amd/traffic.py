@@ -43,7 +43,7 @@ COPY_KERNEL = "copy_kernel"
 
 # Kernel-name fragments of each bench configuration's launches.
 KERNEL_OF = {
-    "rope_llama3": "rope_tok_kernel",
+    "rope_llama3": "rope_tok",
     "rmsnorm_weighted": "rowwise_kernel",
     "cumsum_probs": "scan_",
     "matmul_std002": "gemm_kernel",
@@ -70,22 +70,26 @@ def copy_bytes(cfg: dict) -> int:
     return 64 << 20
 
 
-def run(spec: str, steps: int) -> None:
+def run(spec: str, steps: int, variant: int | None = None, tiles: list[int] | None = None) -> None:
     import torch
 
     import bench
     from enzyme_amd import hip
 
-    cfg = _config(spec)
-    us, _, _, _ = bench.measure(cfg, steps, 2)
+    cfg = dict(_config(spec))
+    if variant is not None:
+        cfg["variant"] = variant
+    if tiles:
+        cfg["tiles"] = tuple(tiles)
+    us, _, _, _, _ = bench.measure(cfg, steps, 2, 0.0)
     nbytes = copy_bytes(cfg)
     src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     for _ in range(steps):
         hip.copy(src, dst)
     torch.cuda.synchronize()
-    print(json.dumps({"spec": spec, "steps": steps, "us_per_launch": round(us, 3),
-                      "copy_bytes": nbytes}), flush=True)
+    print(json.dumps({"spec": spec, "hw_variant": cfg["variant"], "tiles": list(cfg["tiles"]), "steps": steps,
+                      "us_per_launch": round(us, 3), "copy_bytes": nbytes}), flush=True)
 
 
 def _counter_rows(path: Path) -> list[dict]:
@@ -167,6 +171,8 @@ def main(argv=None) -> int:
     r = sub.add_parser("run")
     r.add_argument("spec")
     r.add_argument("--steps", type=int, default=20)
+    r.add_argument("--variant", type=int, default=None, help="hw variant (default: bench.py's)")
+    r.add_argument("--tiles", type=int, nargs="+", default=None, help="tile tuple (default: bench.py's)")
     s = sub.add_parser("summarize")
     s.add_argument("spec")
     s.add_argument("--fetch", type=Path, required=True)
@@ -174,7 +180,7 @@ def main(argv=None) -> int:
     s.add_argument("--out", type=Path, default=REPO / "profiles")
     a = ap.parse_args(argv)
     if a.cmd == "run":
-        run(a.spec, a.steps)
+        run(a.spec, a.steps, a.variant, a.tiles)
     else:
         print(json.dumps(summarize(a.spec, a.fetch, a.write, a.out), indent=1))
     return 0

@@ -23,9 +23,19 @@ def test_rope_split(sizes):
     assert check_parity("rope", sizes, rtol=7.8125e-3, atol=2e-2, budget=12 if sizes[1] > 10000 else 0)
 
 
-@pytest.mark.parametrize("sizes", [(1, 4096, 32, 8, 128), (2, 17, 4, 2, 64), (1, 5, 3, 1, 6)])
+@pytest.mark.parametrize("sizes", [(1, 4096, 32, 8, 128), (2, 17, 4, 2, 64), (1, 5, 3, 1, 6), (3, 5, 4, 2, 128)])
 def test_rope_llama3(sizes):
     assert check_parity("rope_llama3", sizes, rtol=1e-2, atol=1e-2, budget=10)
+
+
+@pytest.mark.parametrize("sizes", [(1, 4096, 32, 8, 128), (3, 5, 4, 2, 128), (2, 17, 4, 2, 64)])
+def test_rope_llama3_token_groups(sizes):
+    """hw variant 1 (token-aligned workgroups, cos/sin rows in LDS) at every
+    tokens-per-workgroup count: ragged last workgroups, and positions that
+    wrap inside one workgroup (b > 1 with s < 16)."""
+    for tpb in (1, 2, 4, 8, 16):
+        for w in (1, 4):
+            assert check_parity("rope_llama3", sizes, rtol=1e-2, atol=1e-2, variants=[1], tiles=(w, tpb)) == 1
 
 
 @pytest.mark.parametrize("sizes", [(128, 8192), (5, 37)])
