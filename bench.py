@@ -75,7 +75,7 @@ METRIC = "achieved HBM GB/s (% peak) per norm/rope/scan; MFMA TFLOP/s for matmul
 # 1.5e-1 in eval/sizes.json).
 CONFIGS = [
     dict(
-        spec="rope_llama3", sizes=(1, 4096, 32, 8, 128), variant=0, tiles=(4, 1), bound="hbm",
+        spec="rope_llama3", sizes=(1, 4096, 32, 8, 128), variant=1, tiles=(16, 8), bound="hbm",
         work=88_080_384, rtol=1e-2, atol=1e-2,
         label="RoPE Llama-3-8B: q[1,4096,32,128] k[1,4096,8,128] bf16, cos/sin[4096,128] fp32, theta 500000",
     ),
@@ -85,7 +85,7 @@ CONFIGS = [
         label="RMSNorm x[2048,4096] bf16, weight[4096] bf16, eps 1e-6",
     ),
     dict(
-        spec="cumsum_probs", sizes=(64, 128256), variant=2, tiles=(8, 4), bound="hbm",
+        spec="cumsum_probs", sizes=(64, 128256), variant=2, tiles=(4, 8), bound="hbm",
         work=65_667_072, rtol=1e-5, atol=0.0,
         label="cumsum over vocab: probs[64,128256] fp32 (sorted softmax of N(0,3) logits)",
     ),
