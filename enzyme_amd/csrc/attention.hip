@@ -666,7 +666,10 @@ __global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
 
 // Merges the key ranges of hw variant 3, one wave per query row (two of
 // the 128 output columns per lane): with M the largest running max,
-// O = sum_r 2^(m_r - M) O_r / sum_r 2^(m_r - M) l_r.
+// O = sum_r 2^(m_r - M) O_r / sum_r 2^(m_r - M) l_r. Lane r < nsplit loads
+// range r's (max, sum) pair, so the weights take one load and two wave
+// reductions; the output columns of the ranges are then loaded four at a
+// time.
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ o_part,
                                                            const float* __restrict__ ml_part,
                                                            bf16* __restrict__ o, int nsplit,
@@ -674,16 +677,18 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
-  float mx = -INFINITY;
-  for (int r = 0; r < nsplit; ++r) mx = fmaxf(mx, ml_part[(r * rows + row) * 2]);
-  float l = 0.f, o0 = 0.f, o1 = 0.f;
+  float2 ml = make_float2(-INFINITY, 0.f);
+  if (lane < nsplit) ml = *reinterpret_cast<const float2*>(ml_part + (lane * rows + row) * 2);
+  const float mx = wave_max(ml.x);
+  const float w = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
+  const float l = wave_sum(w * ml.y);
+  float o0 = 0.f, o1 = 0.f;
+#pragma unroll 4
   for (int r = 0; r < nsplit; ++r) {
-    const float2 ml = *reinterpret_cast<const float2*>(ml_part + (r * rows + row) * 2);
-    const float w = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
+    const float wr = __shfl(w, r, 64);
     const float2 v = *reinterpret_cast<const float2*>(o_part + (r * rows + row) * D + 2 * lane);
-    l += w * ml.y;
-    o0 += w * v.x;
-    o1 += w * v.y;
+    o0 += wr * v.x;
+    o1 += wr * v.y;
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   bf16 out[2] = {static_cast<bf16>(o0 * inv), static_cast<bf16>(o1 * inv)};
