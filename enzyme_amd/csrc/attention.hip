@@ -378,7 +378,7 @@ __global__ __launch_bounds__(W * 64) void attn_kernel(AttnArgs a) {
 // a wave skips the compute of blocks past its last query (it still stages
 // K and V and meets the barrier with the others).
 template <int W, int TN, bool CAUSAL, bool KT, bool SPLIT>
-__global__ __launch_bounds__(W * 64) void attn_sp_kernel(AttnArgs a) {
+__global__ __launch_bounds__(W * 64, W == 4 ? 2 : 1) void attn_sp_kernel(AttnArgs a) {
   constexpr int NT = W * 64;
   constexpr int BQ = 32 * W;
   constexpr int BKV = 32 * TN;
