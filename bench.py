@@ -114,6 +114,7 @@ CONFIGS = [
 ]
 
 SETTLE_MS = 50.0
+_graphs_warm = False
 MAX_SETTLE_LAUNCHES = 200_000
 
 
@@ -158,6 +159,19 @@ def timed_launches(launch, n_sets: int, steps: int, warmup: int, settle_ms: floa
             torch.cuda.synchronize()
             chunk *= 2
     settled = w0.elapsed_time(w1)
+    global _graphs_warm
+    if not _graphs_warm:
+        # The first graph replayed in a process pays a one-time cost (~1.6 ms
+        # measured on the causal attention workload): replay a throwaway
+        # graph of a few launches first, so no timed replay carries it.
+        warm = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(warm):
+            for i in range(min(4, steps)):
+                launch((done + i) % n_sets)
+        warm.replay()
+        torch.cuda.synchronize()
+        del warm
+        _graphs_warm = True
     graph = torch.cuda.CUDAGraph()
     with warnings.catch_warnings(record=True) as caught:
         warnings.simplefilter("always")
