@@ -102,11 +102,10 @@ __global__ __launch_bounds__(1024) void rope_tok_kernel(
 // fetched again by the neighbouring workgroup on another XCD: 52.9 MB read
 // against 46.1 MB at the Llama-3-8B shape). Slot i of the workgroup is (token
 // i / (nh * J), head, pair slice j), j fastest, as in variant 0 with H = 1; a
-// thread walks its slots in chunks of U whose x loads are all issued before
-// any arithmetic. The first chunk's loads are issued before the LDS barrier.
-constexpr int kRopeU = 4;
-
-template <typename T>
+// thread walks its slots in chunks of U (1-4, the fewest that cover its
+// slots in one chunk when they fit) whose x loads are all issued before any
+// arithmetic. The first chunk's loads are issued before the LDS barrier.
+template <typename T, int kRopeU>
 __global__ __launch_bounds__(1024) void rope_tokgroup_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const float* __restrict__ cs,
     const float* __restrict__ sn, T* __restrict__ qo, T* __restrict__ ko, int64_t tokens,
@@ -342,8 +341,15 @@ int launch_tok_t(const Call& c, const void* const* in, void* const* out, hipStre
       return AXON_EINVAL;
     }
     const int64_t blocks = (tokens + TPB - 1) / TPB;
-    hipLaunchKernelGGL(rope_tokgroup_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(bd), lds, st, q,
-                       k, cs, sn, qo, ko, tokens, s, hq, hkv, d, TPB);
+    // Slots per chunk: enough to cover a workgroup's slots in one chunk when
+    // they fit in 4 (fewer idle slots than a fixed 4), else chunks of 4.
+    const int64_t per_thread = (static_cast<int64_t>(TPB) * (hq + hkv) * ((d / 2) / E) + bd - 1) / bd;
+    auto fn = per_thread <= 1 ? rope_tokgroup_kernel<T, 1>
+              : per_thread == 2 ? rope_tokgroup_kernel<T, 2>
+              : per_thread == 3 ? rope_tokgroup_kernel<T, 3>
+                                : rope_tokgroup_kernel<T, 4>;
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(bd), lds, st, q, k, cs, sn, qo, ko, tokens,
+                       s, hq, hkv, d, TPB);
     return launch_status("rope_tokgroup_kernel");
   }
   if (vec) {
