@@ -1346,6 +1346,54 @@ int manifest_mm(int, const int64_t* dims, int, Constraint* out, int cap) {
   return 3;
 }
 
+// Occupancy box of a split-K GEMM (C[m, n] over K). The budgeted selection
+// (src/axon/candidate_filter.py:106-173 of the reference) seeds the corners of
+// the admitted box first, so with three tile arguments and the default budget
+// of 8 it benches only corners: over the full 64..256 x 64..256 x 256..K box
+// those are the 64 x 64 tiles with one K range (too little work per
+// workgroup) and the 256 x 256 tiles over all of K (a handful of workgroups on
+// 256 CUs). The box is therefore capped where a workgroup grid stops filling
+// the chip: BM x BN is the largest output tile (squarest on ties) that still
+// leaves kMinOutputTiles tiles, and the K range the deepest power-of-two
+// multiple of 256 that still gives those tiles kMinGroups workgroups. A
+// shape too small for either keeps the 64-wide tile and one K unit. Tuples
+// outside the box stay legal (check_gemm_shape accepts them) and reachable
+// with the candidate filter off.
+constexpr int64_t kMinOutputTiles = 32;
+constexpr int64_t kMinGroups = 256;
+
+int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+void cap_for_occupancy(int64_t m, int64_t n, int64_t K, Constraint* out) {
+  m = std::max<int64_t>(m, 1);
+  n = std::max<int64_t>(n, 1);
+  int64_t bm = 64, bn = 64, tiles = cdiv64(m, 64) * cdiv64(n, 64);
+  for (const int64_t a : {64, 128, 256})
+    for (const int64_t b : {64, 128, 256}) {
+      const int64_t t = cdiv64(m, a) * cdiv64(n, b);
+      const bool larger = a * b > bm * bn || (a * b == bm * bn && std::llabs(a - b) < std::llabs(bm - bn));
+      if (t >= kMinOutputTiles && larger) {
+        bm = a;
+        bn = b;
+        tiles = t;
+      }
+    }
+  const int64_t kext = k_extent(K);
+  int64_t range = kKUnit;
+  while (range * 2 <= kext && tiles * cdiv64(std::max<int64_t>(K, 1), range * 2) >= kMinGroups) range *= 2;
+  out[0].extent = std::min(out[0].extent, bm);
+  out[1].extent = std::min(out[1].extent, bn);
+  out[2].extent = std::min(out[2].extent, range);
+}
+
+// Manifest of the plain split-K GEMMs (matmul, rmsnorm_matmul, qkv_cte):
+// every legal tuple inside the occupancy box.
+int manifest_splitk(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
+  const int n = manifest_mm(v, dims, dt, out, cap);
+  if (n == 3) cap_for_occupancy(dims[0], dims[1], dims[2], out);
+  return n;
+}
+
 // The plain matmul families have a third hw variant (direct-to-LDS loads)
 // that needs whole 64-deep K steps.
 constexpr int kDmaVariant = 2;
@@ -1388,7 +1436,7 @@ int check_plain(const Call& c, std::string* why) {
 
 int manifest_plain(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   const int64_t mnk[3] = {dims[0], dims[1], dt == AXON_F32 ? 3 * dims[2] : dims[2]};
-  const int n = manifest_mm(v, mnk, dt, out, cap);
+  const int n = manifest_splitk(v, mnk, dt, out, cap);
   if (v == kDmaVariant && (dims[2] % BK != 0 || dt == AXON_F32))
     for (int i = 0; i < n; ++i) out[i].extent = 0;  // admits no tile
   return n;
@@ -1634,7 +1682,7 @@ int check_qkv(const Call& c, std::string* why) {
 
 int manifest_qkv(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   const int64_t mnk[3] = {dims[0], dims[1], dt == AXON_F32 ? 3 * dims[2] : dims[2]};
-  const int n = manifest_mm(v, mnk, dt, out, cap);
+  const int n = manifest_splitk(v, mnk, dt, out, cap);
   // The fused variant has no fp32 instantiation: an extent of 0 admits no tile.
   if (v == kQkvFused && dt != AXON_BF16)
     for (int i = 0; i < n; ++i) out[i].extent = 0;
@@ -2120,7 +2168,7 @@ const char* summary_attn_qkv(int variant) {
 #define AXON_MM_FAMILY(fn_name, spec_name, EPI)                                                \
   const Family* fn_name() {                                                                  \
     static const Family f = {spec_name,     2,           2,         1,           3,          \
-                             kTileArgs3,    3,           summary_mm, manifest_mm, check_mm<EPI>, \
+                             kTileArgs3,    3,           summary_mm, manifest_splitk, check_mm<EPI>, \
                              workspace_mm<EPI>, outputs_mm, launch_mm<EPI>};                  \
     return &f;                                                                               \
   }

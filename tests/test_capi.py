@@ -88,13 +88,23 @@ def test_manifest_literal_reads_back(tmp_path):
     assert cons == tuple(sorted(hip.manifest("matmul_std002", 0, [1024, 512, 16384], hip.AXON_BF16),
                                 key=lambda c: c.tile_arg))
     k = {c.tile_arg: c for c in cons}["TILES_IN_BLOCK_K"]
-    # The last K range may be ragged, so the K range need not divide k.
-    assert not k.require_divisible and k.tile_size == 256 and k.extent == 16384
+    # The last K range may be ragged, so the K range need not divide k. The
+    # occupancy box caps it at 2048: 128 x 128 tiles give 32 output tiles,
+    # and 8 ranges of 2048 give them 256 workgroups.
+    assert not k.require_divisible and k.tile_size == 256 and k.extent == 2048
+
+
+# Families whose manifest admits the legal tuples inside an occupancy box
+# (output tile and K range capped where the workgroup grid stops filling the
+# chip); every other family's manifest admits exactly the legal tuples.
+SPLITK_BOX = {"matmul", "matmul_std002", "rmsnorm_matmul", "rmsnorm_matmul_eps", "qkv_cte"}
 
 
 def test_legal_tiles_are_a_subset_of_the_manifest():
     """Every tile tuple the library accepts passes the manifest the emitter
-    writes (the filter never hides a legal instantiation)."""
+    writes (the filter never hides a legal instantiation), except, for the
+    split-K GEMMs, tuples beyond the occupancy box: those fail only an extent
+    cap, never divisibility, and the box keeps its (1, 1, 1) corner."""
     from axon.candidate_filter import rejection_reason
 
     cases = {"rmsnorm": [2048, 4096], "cumsum_probs": [64, 128256], "rope_llama3": [1, 4096, 32, 8, 128],
@@ -113,7 +123,39 @@ def test_legal_tiles_are_a_subset_of_the_manifest():
             # ranges above 16384 query rows.
             assert legal or any(c.extent == 0 for c in cons), (name, v)
             for t in legal:
-                assert rejection_reason(spec.tile_args, t, cons) is None, (name, v, t)
+                why = rejection_reason(spec.tile_args, t, cons)
+                if name in SPLITK_BOX:
+                    assert why is None or " > extent " in why, (name, v, t, why)
+                else:
+                    assert why is None, (name, v, t, why)
+            if name in SPLITK_BOX and legal:
+                assert rejection_reason(spec.tile_args, (1, 1, 1), cons) is None, (name, v)
+
+
+@pytest.mark.parametrize(
+    ("name", "dims", "best"),
+    [
+        ("matmul_std002", [1024, 512, 16384], (2, 2, 8)),
+        ("rmsnorm_matmul_eps", [1024, 512, 16384], (2, 2, 8)),
+        ("qkv_cte", [16384, 512, 8192], (4, 4, 16)),
+    ],
+)
+def test_default_budget_benches_the_fastest_tuple(name, dims, best):
+    """The reference's default flow (manifest filter, then select_diverse with
+    a budget of 8 per hw variant, src/axon/bench_runner.py:613-621) benches
+    the tuple that a full sweep of every legal tuple of every hw variant
+    measured fastest on MI355X at these shapes. Over the uncapped box the
+    budget reaches only its corners (1x1x32 at 57.5 us against 2x2x8 at
+    34.2 us for the 1024x512x16384 matmul)."""
+    from axon.candidate_filter import rejection_reason, select_diverse
+    from enzyme_amd.kernel_spec import SEED
+
+    spec = load_spec(name)
+    for v in range(hip.variant_count(name)):
+        cons = hip.manifest(name, v, dims, hip.AXON_BF16)
+        legal = [t for t in product(spec.tile_options, repeat=len(spec.tile_args))
+                 if rejection_reason(spec.tile_args, t, cons) is None]
+        assert best in select_diverse(legal, budget=8, seed=SEED), (name, v, legal)
 
 
 def test_manifest_admits_only_legal_tiles():
