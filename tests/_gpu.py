@@ -65,3 +65,26 @@ def check_parity(name, sizes, *, rtol, atol, variants=None, budget=0, dtype=None
             checked += 1
     assert checked, f"{name}: no hw variant has a legal tile tuple for {sizes}"
     return checked
+
+
+def silu_mlp_bound(x, w1, w2, w3, ref):
+    """Elementwise error bound for silu_mlp's bf16 output at unscaled inputs:
+    the bf16 rounding of the output (2^-8 |ref|) plus 2^-14 of the last dot
+    product's scale S = sqrt((h * h) @ (w3 * w3)), h = silu(x @ w1) * (x @ w2),
+    all in float64 from the given inputs. The kernel's measured excess over
+    2^-8 |ref| at the 1024^4 case is below 7e-6 S."""
+    x, w1, w2, w3 = (t.detach().cpu().double() for t in (x, w1, w2, w3))
+    a = x @ w1
+    h = a / (1.0 + torch.exp(-a)) * (x @ w2)
+    return 2.0**-8 * ref.detach().cpu().double().abs() + 2.0**-14 * torch.sqrt((h * h) @ (w3 * w3))
+
+
+def assert_within(got, ref, bound, what):
+    """|got - ref| <= bound elementwise (float64 on the host); names the worst
+    element on failure."""
+    err = (got.detach().cpu().double() - ref.detach().cpu().double()).abs()
+    worst = int(torch.argmax(torch.nan_to_num(err - bound, nan=float("inf"))))
+    assert bool((err <= bound).all()), (
+        f"{what}: |err| {err.flatten()[worst].item():.4g} > bound {bound.flatten()[worst].item():.4g} "
+        f"at flat index {worst}")
+

@@ -4,9 +4,11 @@ tuples each, against the spec's own torch_ref run in fp32 on the GPU on the
 same seeded inputs (the reference's rule: case_gen.py:190-226 coerces inputs
 to fp32; bench_runner.py:703-717 compares with np.allclose). Tolerance: the
 case's rtol/atol; a case without one (a bench-only case in the reference) is
-held to rtol 1e-2 with atol max(1e-2, 1e-3 * max|ref|), a normwise bound,
-because silu_mlp's unscaled N(0, 1) inputs give outputs up to ~1e5 whose
-fp32 summation-order noise alone exceeds an absolute 1e-2. Cases whose
+held to rtol = atol = 1e-2, except silu_mlp sq1k: its unscaled N(0, 1)
+inputs give outputs up to ~1e5, where a uniform absolute 1e-2 is below the
+rounding of the fp32 intermediate, so it is held elementwise to the bf16
+output rounding plus 2^-14 of the last dot product's scale
+(tests/_gpu.py silu_mlp_bound). Cases whose
 inputs exceed 2^28 elements are covered by the dedicated tests of their
 family at full size (test_gpu_qkv.py, test_gpu_composite.py) and skipped
 here to keep the input generation short."""
@@ -19,7 +21,7 @@ import torch
 
 from enzyme_amd import hip
 from enzyme_amd.candidate_filter import select_diverse
-from tests._gpu import legal_tiles
+from tests._gpu import assert_within, legal_tiles, silu_mlp_bound
 from tests._specs import REPO, as_tuple, load_spec, spec_inputs, to_device
 
 pytestmark = pytest.mark.gpu
@@ -55,10 +57,13 @@ def test_reference_case(name, cid):
     codes = [hip.dtype_code(t) for t in dev]
     dvals = [dims[d] for d in spec.dim_vars]
     want = _torch_ref_gpu(spec, dev)
+    bound = None
     if stated:
         rtol, atol = case["rtol"], case["atol"]
+    elif name == "silu_mlp":
+        bound = silu_mlp_bound(*dev, want[0])
     else:
-        rtol, atol = 1e-2, max(1e-2, 1e-3 * max(float(w.abs().max()) for w in want))
+        rtol, atol = 1e-2, 1e-2
     checked = 0
     for v in range(hip.variant_count(name)):
         tiles = legal_tiles(name, v, dvals, codes, len(spec.tile_args), options=spec.tile_options)
@@ -69,6 +74,9 @@ def test_reference_case(name, cid):
             ln.launch()
             torch.cuda.synchronize()
             for i, (got, ref) in enumerate(zip(ln.outputs, want)):
+                if bound is not None:
+                    assert_within(got, ref, bound, f"{name}/{cid} v{v} tiles {t} out{i}")
+                    continue
                 torch.testing.assert_close(got.float(), ref.float(), rtol=rtol, atol=atol,
                                            msg=lambda m, v=v, t=t, i=i: f"{name}/{cid} v{v} tiles {t} out{i}: {m}")
             checked += 1

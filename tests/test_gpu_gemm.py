@@ -12,9 +12,12 @@ reference's fp32 tolerance rtol = atol = 1e-3 at its ck_16k_l2 shape
 (1024 x 1024 x 16384) and at ragged shapes.
 
 silu_mlp with the spec's unscaled N(0, 1) inputs has outputs up to ~1e5, so
-an absolute 1e-2 is below fp32 summation-order noise there; that case is
-held to rtol 1e-2 with atol 1e-3 * max|ref| (a normwise bound), and a scaled
-case (w ~ N(0, 1/fan_in)) is held to the plain 1e-2 / 1e-2."""
+a uniform absolute 1e-2 is below the rounding of its fp32 intermediate
+there. That case is held elementwise to the bf16 output rounding plus a
+term on the dot product's own scale: |got - ref| <= 2^-8 |ref| + 2^-14 S,
+S = sqrt((h * h) @ (w3 * w3)) with h = silu(x @ w1) * (x @ w2); the kernel's
+measured excess over 2^-8 |ref| is below 7e-6 S. A scaled case
+(w ~ N(0, 1/fan_in)) is held to the plain 1e-2 / 1e-2."""
 
 import numpy as np
 import pytest
@@ -67,13 +70,29 @@ def test_gemm_repeated_launches_bit_identical(variant):
     assert torch.equal(first, ln.outputs[0])
 
 
-def test_silu_mlp_unscaled_normwise():
+def test_silu_mlp_unscaled_elementwise():
+    """The spec's sq1k case (N(0, 1) inputs) in every hw variant over a
+    diverse tile selection, elementwise against the oracle."""
+    from enzyme_amd.candidate_filter import select_diverse
+    from tests._gpu import assert_within, legal_tiles, silu_mlp_bound
     from tests._specs import spec_inputs, to_device
 
-    spec, dims, host = spec_inputs("silu_mlp", (1024, 1024, 1024, 1024))
-    ref = oracle.silu_mlp(*[torch.as_tensor(np.asarray(a)) if not isinstance(a, torch.Tensor) else a for a in host])
-    assert check_parity("silu_mlp", (1024, 1024, 1024, 1024), rtol=1e-2,
-                        atol=float(1e-3 * ref.abs().max()), budget=6, want=(ref,))
+    sizes = (1024, 1024, 1024, 1024)
+    spec, dims, host = spec_inputs("silu_mlp", sizes)
+    dev = to_device(host)
+    ref = oracle.silu_mlp(*[t.cpu() for t in dev])
+    bound = silu_mlp_bound(*dev, ref)
+    codes = [hip.dtype_code(t) for t in dev]
+    checked = 0
+    for v in range(hip.variant_count("silu_mlp")):
+        for t in select_diverse(legal_tiles("silu_mlp", v, list(sizes), codes, 4), budget=6, seed=42):
+            ln = hip.Launcher("silu_mlp", v, t, list(sizes), dev)
+            ln.outputs[0].fill_(float("nan"))
+            ln.launch()
+            torch.cuda.synchronize()
+            assert_within(ln.outputs[0], ref, bound, f"silu_mlp v{v} tiles {t}")
+            checked += 1
+    assert checked
 
 
 def test_silu_mlp_scaled_elementwise():
