@@ -204,6 +204,48 @@ def test_manifest_admits_only_legal_tiles():
     assert checked > 500
 
 
+# Small legal dims per spec; the first dim is set to 0 below.
+_EMPTY_DIMS = {"attention_causal": [1, 2, 64, 128], "attention_nkilib": [64, 128],
+               "rope_llama3": [1, 64, 4, 2, 128], "rope": [64, 128]}
+
+
+def test_empty_leading_dimension_is_a_no_op():
+    """Every family, every hw variant, both launch entry points: with the
+    leading dim 0 every output is empty, and the launch returns AXON_OK
+    before touching any pointer, stream or workspace (so null pointers and no
+    workspace are accepted and nothing reaches the GPU)."""
+    import ctypes
+
+    from enzyme_amd.dtypes import to_torch
+    from tests._specs import spec_inputs
+
+    names = sorted(p.name for p in KERNELS.iterdir() if (p / "__init__.py").exists())
+    checked = 0
+    for name in names:
+        spec = load_spec(name)
+        _, _, ins = spec_inputs(name, tuple([8] * len(spec.dim_vars)) if name not in _EMPTY_DIMS
+                                else tuple(min(d, 128) if d else 8 for d in _EMPTY_DIMS[name]))
+        codes = [hip.dtype_code(to_torch(a)) for a in ins]
+        dims = [0] + list(_EMPTY_DIMS.get(name, [64] * len(spec.dim_vars)))[1:]
+        for v in range(hip.variant_count(name)):
+            tiles = next(t for t in product(spec.tile_options, repeat=len(spec.tile_args))
+                         if hip.check(name, v, t, dims, codes)[0] == hip.AXON_OK)
+            ct = (ctypes.c_int32 * len(tiles))(*tiles)
+            cd = (ctypes.c_int64 * len(dims))(*dims)
+            cc = (ctypes.c_int32 * len(codes))(*codes)
+            n_in, n_out = len(spec.input_specs), len(hip.outputs(name, dims, codes))
+            nulls_in = (ctypes.c_void_p * n_in)()
+            nulls_out = (ctypes.c_void_p * n_out)()
+            rc = hip.lib().axon_variant_launch(name.encode(), v, ct, len(tiles), cd, len(dims), cc, len(codes),
+                                               nulls_in, n_in, nulls_out, n_out, None, 0, None)
+            assert rc == hip.AXON_OK, (name, v, tiles, hip.last_error())
+            rc = hip.lib().axon_variant_launch_noalloc(name.encode(), v, ct, len(tiles), cd, len(dims), cc,
+                                                       len(codes), nulls_in, n_in, nulls_out, n_out, None)
+            assert rc == hip.AXON_OK, (name, v, tiles, hip.last_error())
+            checked += 1
+    assert checked >= len(names)
+
+
 def test_compile_worker_plans_legal_and_asserts_illegal(tmp_path):
     spec = load_spec("rmsnorm")
     mod = tmp_path / "rmsnorm__v0_t0.py"
