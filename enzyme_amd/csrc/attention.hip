@@ -971,9 +971,9 @@ int launch_common(const Call& c, const void* const* in, void* const* out, void* 
   a.s = static_cast<int>(s);
   a.bh = static_cast<int>(bh);
   a.qblocks = static_cast<int>((s + 32 * W * QT - 1) / (32 * W * QT));
-  if (static_cast<int64_t>(a.qblocks) * a.bh > (1LL << 31) - 1) {
-    set_error("grid too large");
-    return AXON_EINVAL;
+  {
+    const int rc = grid_check("attn_kernel", static_cast<int64_t>(a.qblocks) * a.bh, 1, W * 64);
+    if (rc != AXON_OK) return rc;
   }
   // Deal heads to XCDs (workgroup b runs on XCD b % 8) when they split evenly.
   a.xcd_heads = a.bh % kXcds == 0 ? a.bh / kXcds : 0;
@@ -988,10 +988,9 @@ int launch_common(const Call& c, const void* const* in, void* const* out, void* 
     a.kv_split = p.kv_split;
     a.o_part = static_cast<float*>(ws);
     a.ml_part = reinterpret_cast<float*>(static_cast<char*>(ws) + ml_off);
-    if (static_cast<int64_t>(a.qblocks) * a.bh * a.nsplit > (1LL << 31) - 1) {
-      set_error("grid too large");
-      return AXON_EINVAL;
-    }
+    int rc = grid_check("attn_sp_kernel", static_cast<int64_t>(a.qblocks) * a.bh * a.nsplit, 1, W * 64);
+    if (rc == AXON_OK) rc = grid_check("attn_combine_kernel", (bh * s + 3) / 4, 1, 256);
+    if (rc != AXON_OK) return rc;
   }
   if (causal) {
     a.scale_log2 = kLog2e / sqrtf(static_cast<float>(D));

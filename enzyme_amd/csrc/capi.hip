@@ -112,6 +112,14 @@ int checked(const char* kernel, const Call& c, const Family** f) {
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
+int grid_check(const char* what, int64_t gx, int64_t gy, int64_t threads) {
+  if (grid_fits(gx, gy, threads)) return AXON_OK;
+  set_error(std::string(what) + ": " + std::to_string(gx) + " x " + std::to_string(gy) + " workgroups of " +
+            std::to_string(threads) +
+            " threads exceed one dispatch (at most 2^31 - 1 x 65535 workgroups, fewer than 2^32 work-items)");
+  return AXON_EINVAL;
+}
+
 int launch_status(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -438,10 +446,9 @@ int axon_copy_shape(const void* src, void* dst, size_t bytes, int shape, axon_st
   if (shape == 1 || shape == 2) {
     const int V = shape == 1 ? 8 : 4;
     const size_t blocks = (n16 + 256 * V - 1) / (256 * V);
-    if (blocks > 0x7fffffffu) {
-      set_error("axon_copy_shape: copy too large for a one-shot grid");
-      return AXON_EARG;
-    }
+    if (const int rc = grid_check("axon_copy_shape (one-shot)", static_cast<int64_t>(blocks), 1, 256);
+        rc != AXON_OK)
+      return rc;
     if (V == 8)
       hipLaunchKernelGGL(copy_oneshot_kernel<8>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                          st, s, d, n16);

@@ -249,6 +249,8 @@ int launch_rope_t(const Call& c, const void* const* in, void* const* out, hipStr
     aligned = aligned && aligned16(ptr);
   const int64_t vecs = (len + E - 1) / E;
   const int64_t per_block = static_cast<int64_t>(V) * W * kWave;
+  const int rc = grid_check("rope_split_kernel", (vecs + per_block - 1) / per_block, 1, W * kWave);
+  if (rc != AXON_OK) return rc;
   const dim3 grid(static_cast<unsigned>((vecs + per_block - 1) / per_block)), block(W * kWave);
   if (aligned)
     hipLaunchKernelGGL((rope_fn<T, true>(V)), grid, block, 0, st, a, b, cs, sn, oe, oo, len);
@@ -296,6 +298,8 @@ int launch_adam_t(const Call& c, const void* const* in, void* const* out, hipStr
   for (int i = 0; i < 3; ++i) aligned = aligned && aligned16(o[i]);
   const int64_t vecs = (len + E - 1) / E;
   const int64_t per_block = static_cast<int64_t>(V) * W * kWave;
+  const int rc = grid_check("adam_kernel", (vecs + per_block - 1) / per_block, 1, W * kWave);
+  if (rc != AXON_OK) return rc;
   const dim3 grid(static_cast<unsigned>((vecs + per_block - 1) / per_block)), block(W * kWave);
   if (aligned)
     hipLaunchKernelGGL((adam_fn<T, true>(V)), grid, block, 0, st, x[0], x[1], x[2], x[3], x[4],

@@ -1129,8 +1129,9 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, st
     return AXON_EINVAL;
   }
   const Plan p = plan_of(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), tm, tn, tk);
-  if (static_cast<int64_t>(p.S) * p.MT * p.NT > (1LL << 31) - 1) {
-    *why = "grid too large";
+  if (!grid_fits(static_cast<int64_t>(p.S) * p.MT * p.NT, 1, kThreads) ||
+      (p.S > 1 && !grid_fits((M * N / 4 + 255) / 256, 1, 256))) {
+    *why = "grid too large for one dispatch (fewer than 2^32 work-items)";
     return AXON_EINVAL;
   }
   return AXON_OK;
@@ -1202,8 +1203,18 @@ void launch_dma_tile(const GemmArgs& g, hipStream_t st) {
   }
 }
 
+// One GEMM launch's grids (the main kernel and, with split K, the fixup) fit
+// one dispatch each.
+int gemm_grid_check(const GemmArgs& g) {
+  int rc = grid_check("gemm_kernel", static_cast<int64_t>(g.S) * g.MT * g.NT, 1, kThreads);
+  if (rc == AXON_OK && g.S > 1)
+    rc = grid_check("splitk_reduce_kernel", (static_cast<int64_t>(g.M) * g.N / 4 + 255) / 256, 1, 256);
+  return rc;
+}
+
 template <int EPI>
 int dispatch_dma(int BM, int BN, const GemmArgs& g, hipStream_t st) {
+  if (const int rc = gemm_grid_check(g); rc != AXON_OK) return rc;
 #define AXON_GEMM_CASE(bm, bn) \
   if (BM == bm && BN == bn) { launch_dma_tile<bm, bn, EPI>(g, st); return launch_status("gemm_dma_kernel"); }
   AXON_GEMM_CASE(64, 64)
@@ -1225,6 +1236,7 @@ constexpr int deep_pd(int BM, int BN) { return BM * BN <= 128 * 128 ? 3 : 2; }
 
 template <int EPI, bool AF>
 int dispatch(int BM, int BN, const GemmArgs& g, hipStream_t st, int variant = 0) {
+  if (const int rc = gemm_grid_check(g); rc != AXON_OK) return rc;
 #define AXON_GEMM_CASE(bm, bn)                                           \
   if (BM == bm && BN == bn) {                                            \
     if (variant == 1) launch_tile<bm, bn, EPI, AF, deep_pd(bm, bn)>(g, st); \
@@ -1250,6 +1262,7 @@ int dispatch(int BM, int BN, const GemmArgs& g, hipStream_t st, int variant = 0)
 // 2), so only those shapes are instantiated.
 template <int EPI, bool AF>
 int dispatch_mlp(int BM, int BN, const GemmArgs& g, hipStream_t st) {
+  if (const int rc = gemm_grid_check(g); rc != AXON_OK) return rc;
 #define AXON_GEMM_CASE(bm, bn) \
   if (BM == bm && BN == bn) { launch_tile<bm, bn, EPI, AF, 1>(g, st); return launch_status("gemm_kernel"); }
   AXON_GEMM_CASE(64, 64)
@@ -1268,6 +1281,7 @@ int dispatch_mlp(int BM, int BN, const GemmArgs& g, hipStream_t st) {
 constexpr int qkv_pd(int BM, int BN) { return BM * BN <= 128 * 128 ? 2 : 1; }
 
 int dispatch_qkv(int BM, int BN, const GemmArgs& g, hipStream_t st) {
+  if (const int rc = gemm_grid_check(g); rc != AXON_OK) return rc;
 #define AXON_GEMM_CASE(bm, bn)                                   \
   if (BM == bm && BN == bn) {                                    \
     launch_tile<bm, bn, kQkv, false, qkv_pd(bm, bn)>(g, st);     \
@@ -1481,9 +1495,12 @@ int launch_plain(const Call& c, const void* const* in, void* const* out, void* w
   bf16* b = reinterpret_cast<bf16*>(base + L.b);
   const int64_t mk = static_cast<int64_t>(m) * k, kn = static_cast<int64_t>(k) * n;
   if (mk > 0) {
+    int rc = grid_check("split_rows_hilo_kernel", (mk / 8 + 255) / 256, 1, 256);
+    if (rc == AXON_OK) rc = grid_check("qkv_split_w_kernel", (kn / 8 + 255) / 256, 1, 256);
+    if (rc != AXON_OK) return rc;
     hipLaunchKernelGGL(split_rows_hilo_kernel, dim3(static_cast<unsigned>((mk / 8 + 255) / 256)), dim3(256), 0,
                        st, static_cast<const float*>(in[0]), a, mk, k);
-    int rc = launch_status("split_rows_hilo_kernel");
+    rc = launch_status("split_rows_hilo_kernel");
     if (rc != AXON_OK) return rc;
     hipLaunchKernelGGL(qkv_split_w_kernel, dim3(static_cast<unsigned>((kn / 8 + 255) / 256)), dim3(256), 0, st,
                        static_cast<const float*>(in[1]), b, kn);
@@ -1744,6 +1761,11 @@ int launch_qkv(const Call& c, const void* const* in, void* const* out, void* ws,
     return dispatch_qkv(L.p.BM, L.p.BN, g, st);
   }
   const bool f32 = c.dtype(0) == AXON_F32;
+  {
+    int rc = grid_check("qkv_prep_kernel", m, 1, kPrepThreads);
+    if (rc == AXON_OK && f32) rc = grid_check("qkv_split_w_kernel", (static_cast<int64_t>(k) * n / 8 + 255) / 256, 1, 256);
+    if (rc != AXON_OK) return rc;
+  }
   char* base = static_cast<char*>(ws);
   float* scale = reinterpret_cast<float*>(base + L.scale);
   bf16* a = reinterpret_cast<bf16*>(base + L.a);
@@ -1852,10 +1874,9 @@ __global__ __launch_bounds__(256) void transpose_bf16_vec_kernel(const bf16* __r
 
 int launch_transpose(const bf16* in, bf16* out, int R, int C, hipStream_t st) {
   if (R == 0 || C == 0) return AXON_OK;
-  if ((C + kTp - 1) / kTp > 65535) {
-    set_error("transpose: more than 65535 column tiles");
-    return AXON_EINVAL;
-  }
+  if (const int rc = grid_check("transpose_bf16_kernel", (R + kTp - 1) / kTp, (C + kTp - 1) / kTp, 256);
+      rc != AXON_OK)
+    return rc;
   const dim3 grid((R + kTp - 1) / kTp, (C + kTp - 1) / kTp);
   const bool vec = R % 8 == 0 && C % 8 == 0 && aligned16(in) && aligned16(out);
   if (vec) hipLaunchKernelGGL(transpose_bf16_vec_kernel, grid, dim3(256), 0, st, in, out, R, C);

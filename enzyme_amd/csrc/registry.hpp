@@ -71,6 +71,17 @@ void set_error(const std::string& msg);
 // Returns AXON_OK or AXON_EHIP after the last enqueue.
 int launch_status(const char* what);
 
+// A dispatch holds at most 2^31 - 1 workgroups along x, at most 65535 along
+// y, and fewer than 2^32 work-items in total.
+inline bool grid_fits(int64_t gx, int64_t gy, int64_t threads) {
+  return gx >= 0 && gy >= 0 && gx <= (1LL << 31) - 1 && gy <= 65535 && threads > 0 &&
+         (gx == 0 || gy == 0 || gx * gy <= 0xFFFFFFFFLL / threads);
+}
+
+// AXON_OK when a launch of gx x gy workgroups of `threads` threads fits one
+// dispatch; otherwise records why (naming `what`) and returns AXON_EINVAL.
+int grid_check(const char* what, int64_t gx, int64_t gy, int64_t threads);
+
 inline bool is_pow2_in(int v, int lo, int hi) {
   return v >= lo && v <= hi && (v & (v - 1)) == 0;
 }

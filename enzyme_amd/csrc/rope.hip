@@ -341,6 +341,8 @@ int launch_tok_t(const Call& c, const void* const* in, void* const* out, hipStre
       return AXON_EINVAL;
     }
     const int64_t blocks = (tokens + TPB - 1) / TPB;
+    const int rc = grid_check("rope_tokgroup_kernel", blocks, 1, bd);
+    if (rc != AXON_OK) return rc;
     // Slots per chunk: enough to cover a workgroup's slots in one chunk when
     // they fit in 4 (fewer idle slots than a fixed 4), else chunks of 4.
     const int64_t per_thread = (static_cast<int64_t>(TPB) * (hq + hkv) * ((d / 2) / E) + bd - 1) / bd;
@@ -358,11 +360,15 @@ int launch_tok_t(const Call& c, const void* const* in, void* const* out, hipStre
     const int J = (d / 2) / E;
     const int64_t slots = tokens * HG * J;
     const int bd = W * kWave;
+    const int rc = grid_check("rope_tok_kernel", (slots + bd - 1) / bd, 1, bd);
+    if (rc != AXON_OK) return rc;
     const dim3 grid(static_cast<unsigned>((slots + bd - 1) / bd));
     hipLaunchKernelGGL((tok_fn<T>(H)), grid, dim3(bd), 0, st, q, k, cs, sn, qo, ko, tokens, s, hq,
                        hkv, d, HG);
   } else {
     const int64_t total = tokens * nh * (d / 2);
+    const int rc = grid_check("rope_tok_scalar_kernel", (total + 255) / 256, 1, 256);
+    if (rc != AXON_OK) return rc;
     const dim3 grid(static_cast<unsigned>((total + 255) / 256));
     hipLaunchKernelGGL(rope_tok_scalar_kernel<T>, grid, dim3(256), 0, st, q, k, cs, sn, qo, ko,
                        tokens, s, hq, hkv, d);

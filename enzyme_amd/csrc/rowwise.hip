@@ -227,6 +227,10 @@ int check_rows(const Call& c, std::string* why) {
     *why = "TILES_IN_BLOCK_N: a row needs more than 16 waves at this vector count";
     return AXON_EINVAL;
   }
+  if (!grid_fits((c.dim(0) + s.R - 1) / s.R, 1, static_cast<int64_t>(s.R) * s.Wr * kWave)) {
+    *why = "too many rows for one dispatch at these tiles (fewer than 2^32 work-items)";
+    return AXON_EINVAL;
+  }
   return AXON_OK;
 }
 
@@ -267,6 +271,8 @@ int launch_typed(const Call& c, const void* const* in, void* const* out, hipStre
   T* y = static_cast<T*>(out[0]);
   const bool aligned = (n % s.E) == 0 && aligned16(x) && aligned16(y) &&
                        (MODE != kRmsWeighted || aligned16(w));
+  const int rc = grid_check("rowwise_kernel", (m + s.R - 1) / s.R, 1, static_cast<int64_t>(s.R) * s.Wr * kWave);
+  if (rc != AXON_OK) return rc;
   const dim3 grid(static_cast<unsigned>((m + s.R - 1) / s.R));
   const dim3 block(static_cast<unsigned>(s.R * s.Wr * kWave));
   if (aligned) {

@@ -387,6 +387,13 @@ int check_scan(const Call& c, std::string* why) {
       return AXON_EINVAL;
     }
   }
+  const int64_t nchunks = c.variant == 0 ? 1 : (c.dim(1) + chunk_elems(c) - 1) / chunk_elems(c);
+  const bool fits = c.variant == 1 ? grid_fits(nchunks, c.dim(0), c.tile(0) * kWave)
+                                   : grid_fits(c.dim(0) * nchunks, 1, c.tile(0) * kWave);
+  if (!fits) {
+    *why = "too many workgroups for one dispatch at these tiles (fewer than 2^32 work-items)";
+    return AXON_EINVAL;
+  }
   return AXON_OK;
 }
 
@@ -449,12 +456,16 @@ int launch_scan_ta(const Call& c, const T* x, T* y, void* ws, hipStream_t st) {
   const int W = c.tile(0), V = c.tile(1);
   const dim3 block(W * kWave);
   if (c.variant == 0) {
+    const int rc = grid_check("scan_rows_kernel", m, 1, W * kWave);
+    if (rc != AXON_OK) return rc;
     hipLaunchKernelGGL((rows_fn<T, A>(V)), dim3(static_cast<unsigned>(m)), block, 0, st, x, y, n);
     return launch_status("scan_rows_kernel");
   }
   const int64_t ce = chunk_elems(c);
   const int nchunks = static_cast<int>((n + ce - 1) / ce);
   if (c.variant == 2) {
+    const int rc = grid_check("scan_onepass_kernel", m * nchunks, 1, W * kWave);
+    if (rc != AXON_OK) return rc;
     const unsigned nblocks = static_cast<unsigned>(m * nchunks);
     unsigned* hdr = static_cast<unsigned*>(ws);
     auto* slots = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + kOnepassHeader);
@@ -463,9 +474,11 @@ int launch_scan_ta(const Call& c, const T* x, T* y, void* ws, hipStream_t st) {
     return launch_status("scan_onepass_kernel");
   }
   double* totals = static_cast<double*>(ws);
+  int rc = grid_check("chunk_total_kernel", nchunks, m, W * kWave);
+  if (rc != AXON_OK) return rc;
   const dim3 grid(nchunks, static_cast<unsigned>(m));
   hipLaunchKernelGGL((tot_fn<T, A>(V)), grid, block, 0, st, x, totals, n, nchunks);
-  const int rc = launch_status("chunk_total_kernel");
+  rc = launch_status("chunk_total_kernel");
   if (rc != AXON_OK) return rc;
   hipLaunchKernelGGL((cscan_fn<T, A>(V)), grid, block, 0, st, x, y, totals, n, nchunks);
   return launch_status("chunk_scan_kernel");

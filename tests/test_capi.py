@@ -246,6 +246,31 @@ def test_empty_leading_dimension_is_a_no_op():
     assert checked >= len(names)
 
 
+@pytest.mark.parametrize(
+    ("name", "tiles", "dims", "dtype", "legal"),
+    [
+        ("rmsnorm", (1, 1), [1 << 27, 8], "bf16", False),     # 2^27 workgroups of 64 threads
+        ("rmsnorm", (16, 1), [1 << 27, 8], "bf16", False),    # 2^23 of 1024
+        ("rmsnorm", (1, 1), [1 << 20, 8], "bf16", True),
+        ("matmul", (1, 1, 1), [32768, 32768, 32768], "bf16", False),  # 33.5 M workgroups of 256
+        ("matmul", (4, 4, 16), [32768, 32768, 32768], "bf16", True),
+        ("cumsum_probs", (16, 1), [1 << 23, 64], "f32", False),      # one 1024-thread workgroup per row
+        ("cumsum_probs", (1, 1), [1 << 20, 64], "f32", True),
+    ],
+)
+def test_oversized_grids_are_refused(name, tiles, dims, dtype, legal):
+    """A dispatch holds fewer than 2^32 work-items: tile tuples whose grid
+    would exceed that at these dims are illegal (the compile worker's
+    "assert"), not launched and truncated."""
+    code = hip.AXON_BF16 if dtype == "bf16" else hip.AXON_F32
+    n_in = len(load_spec(name).input_specs)
+    st, why = hip.check(name, 0, tiles, dims, [code] * n_in)
+    if legal:
+        assert st == hip.AXON_OK, why
+    else:
+        assert st == hip.AXON_EINVAL and "2^32" in why, (st, why)
+
+
 def test_compile_worker_plans_legal_and_asserts_illegal(tmp_path):
     spec = load_spec("rmsnorm")
     mod = tmp_path / "rmsnorm__v0_t0.py"
