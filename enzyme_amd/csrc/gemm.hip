@@ -547,7 +547,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   auto row_of = [&](int i, int e) { return wm * WM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); };
   auto col_of = [&](int j) { return wn * WN + j * 32 + (lane & 31); };
 
+  // An empty contraction (K == 0) leaves zero accumulators and an empty
+  // normalised row, whose product is 0: scale 0 rather than 1/0 or 0/0.
   auto scale_of = [&](float sumsq) -> float {
+    if (g.K == 0) return 0.f;
     if constexpr (EPI == kRmsSum) return 1.f / sqrtf(sumsq);
     else if constexpr (EPI == kSoftmax) return 1.f / sumsq;
     else if constexpr (EPI == kRmsEps || EPI == kQkv) return 1.f / sqrtf(sumsq / static_cast<float>(g.K) + g.eps);
@@ -1023,7 +1026,7 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const T* __restr
     float t = 0.f;
 #pragma unroll
     for (int i = 0; i < kPrepThreads / kWave; ++i) t += part[i];
-    rscale[row] = 1.f / sqrtf(t * (1.f / static_cast<float>(k)) + eps);
+    rscale[row] = k == 0 ? 0.f : 1.f / sqrtf(t * (1.f / static_cast<float>(k)) + eps);
   }
 }
 
@@ -1167,6 +1170,7 @@ void launch_tile(const GemmArgs& g, hipStream_t st) {
     configured.store(true, std::memory_order_release);
   }
   const unsigned blocks = static_cast<unsigned>(g.S * g.MT * g.NT);
+  if (blocks == 0) return;  // an empty output (m or n is 0 inside a composite)
   hipLaunchKernelGGL(fn, dim3(blocks), dim3(kThreads), lds, st, g);
   if (g.S > 1) {
     const int64_t quads = static_cast<int64_t>(g.M) * g.N / 4;
@@ -1195,6 +1199,7 @@ void launch_dma_tile(const GemmArgs& g, hipStream_t st) {
     configured.store(true, std::memory_order_release);
   }
   const unsigned blocks = static_cast<unsigned>(g.S * g.MT * g.NT);
+  if (blocks == 0) return;  // an empty output (m or n is 0 inside a composite)
   hipLaunchKernelGGL(fn, dim3(blocks), dim3(kThreads), lds, st, g);
   if (g.S > 1) {
     const int64_t quads = static_cast<int64_t>(g.M) * g.N / 4;
@@ -1640,18 +1645,21 @@ int launch_mlp(const Call& c, const void* const* in, void* const* out, void* ws,
       set_error("GEMM buffers must be 16-byte aligned");
       return AXON_EARG;
     }
-  if (!aligned16(out[0]) || ws == nullptr) {
+  const MlpLayout L = mlp_layout(c);
+  if (!aligned16(out[0]) || (ws == nullptr && L.h + L.data > 0)) {
     set_error("silu_mlp needs an aligned output and its workspace");
     return AXON_EARG;
   }
-  const MlpLayout L = mlp_layout(c);
   char* base = static_cast<char*>(ws);
   float* H = reinterpret_cast<float*>(base);
   void* data = base + L.h;
-  const GemmArgs g1 = make_args(in[0], static_cast<const bf16*>(in[1]), static_cast<const bf16*>(in[2]),
-                                H, m, n, k, L.p1, data, 2, 0.f);
-  int rc = dispatch_mlp<kSiluMul, false>(L.p1.BM, L.p1.BN, g1, st);
-  if (rc != AXON_OK) return rc;
+  // n == 0: H is empty and the second product (over n) is all zeros.
+  if (n > 0) {
+    const GemmArgs g1 = make_args(in[0], static_cast<const bf16*>(in[1]), static_cast<const bf16*>(in[2]),
+                                  H, m, n, k, L.p1, data, 2, 0.f);
+    const int rc = dispatch_mlp<kSiluMul, false>(L.p1.BM, L.p1.BN, g1, st);
+    if (rc != AXON_OK) return rc;
+  }
   const GemmArgs g2 = make_args(H, static_cast<const bf16*>(in[3]), nullptr, out[0], m, p, n, L.p2,
                                 data, 1, 0.f);
   return dispatch_mlp<kPlain, true>(L.p2.BM, L.p2.BN, g2, st);

@@ -127,3 +127,54 @@ def test_matmul_fp32(sizes):
                         budget=4 if sizes[2] > 10000 else 8)
     codes = [hip.AXON_F32, hip.AXON_F32]
     assert hip.check("matmul", 2, (1, 1, 1), sizes, codes)[0] == hip.AXON_EDTYPE
+
+
+@pytest.mark.parametrize(
+    ("name", "sizes", "empty_dim"),
+    [
+        ("matmul", (64, 128, 0), "k"),
+        ("rmsnorm_matmul", (64, 128, 0), "k"),
+        ("rmsnorm_matmul_eps", (64, 128, 0), "k"),
+        ("softmax_mm", (64, 128, 0), "k"),
+        ("qkv_cte", (64, 128, 0), "k"),
+        ("silu_mlp", (64, 64, 0, 128), "k"),
+        ("silu_mlp", (64, 0, 64, 128), "n"),
+        ("linear_attention", (64, 0, 128, 64), "sk"),
+    ],
+)
+def test_empty_contraction_gives_zeros(name, sizes, empty_dim):
+    """A zero-length contraction with non-empty outputs: the reference's math
+    gives zeros (the normalised or softmaxed row is empty). torch gives
+    zero-element tensors a null data pointer, which the C ABI refuses with
+    AXON_EARG; with valid pointers (larger live buffers, the dims saying the
+    contraction is empty) every hw variant writes exact zeros. With no K step
+    no kernel reads the operands."""
+    from tests._gpu import legal_tiles
+    from tests._specs import load_spec
+
+    print(f"empty contraction {name} {sizes}", flush=True)
+    spec = load_spec(name)
+    dims = dict(zip(spec.dim_vars, sizes))
+    shapes = spec.input_shapes(dims)
+    live = [torch.randn([max(d, 8) for d in shape], device="cuda").to(torch.bfloat16) for shape in shapes]
+    views = [t[tuple(slice(0, d) for d in shape)] for t, shape in zip(live, shapes)]
+    want = oracle.ORACLE[name](*[t.cpu() for t in views])
+    want = want if isinstance(want, tuple) else (want,)
+    assert all(torch.count_nonzero(w) == 0 for w in want)
+    codes = [hip.dtype_code(t) for t in live]
+    checked = 0
+    for v in range(hip.variant_count(name)):
+        for tiles in legal_tiles(name, v, list(sizes), codes, len(spec.tile_args))[:2]:
+            if any(t.data_ptr() == 0 for t in views):
+                with pytest.raises(hip.HipLibraryError) as e:
+                    hip.Launcher(name, v, tiles, list(sizes), views).launch()
+                assert e.value.status == hip.AXON_EARG and "null" in str(e.value), str(e.value)
+            ln = hip.Launcher(name, v, tiles, list(sizes), live)
+            for o in ln.outputs:
+                o.fill_(float("nan"))
+            ln.launch()
+            torch.cuda.synchronize()
+            for o in ln.outputs:
+                assert torch.count_nonzero(o) == 0 and not torch.isnan(o).any(), (name, v, tiles)
+            checked += 1
+    assert checked
