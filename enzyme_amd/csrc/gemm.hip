@@ -122,16 +122,26 @@ using ic = std::integral_constant<int, N>;
 template <int PD>
 constexpr bool rolling() { return PD == 1; }
 
-template <int BM, int BN, int EPI, bool A_F32, int PD>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
+// NTH threads per workgroup: 256 (4 waves as 2 x 2 over the tile) or 512
+// (hw variant 3 of the plain GEMMs, 2 of the RMSNorm GEMMs): two groups of
+// 4 waves on the same 2 x 2 wave tiles, group wk computing the 16-deep
+// k-slices 2 wk and 2 wk + 1 of every 64-deep K step. The 8 waves share the
+// loads (half per thread) and two waves sit on every SIMD, while the LDS
+// fragment reads per step stay those of 4 waves; group 1 adds its
+// accumulators into group 0's through LDS once, after the last step.
+template <int BM, int BN, int EPI, bool A_F32, int PD, int NTH = kThreads>
+__global__ __launch_bounds__(NTH) void gemm_kernel(GemmArgs g) {
   constexpr bool DUAL = EPI == kSiluMul;
+  constexpr int KW = NTH / kThreads;       // k-slice groups of 4 waves
   constexpr int WM = BM / 2, WN = BN / 2;  // per-wave tile
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int AV = BM * BK / 8 / kThreads;  // A vectors per thread (8 k-values each)
-  constexpr int KR = BN / 32;                 // B rows per thread block (k)
-  constexpr int NA = A_F32 ? 2 : 1;           // hi/lo planes for an fp32 A
+  constexpr int AV = BM * BK / 8 / NTH;  // A vectors per thread (8 k-values each)
+  constexpr int KR = BN * BK / 8 / NTH;  // B rows per thread block (k)
+  constexpr int NA = A_F32 ? 2 : 1;      // hi/lo planes for an fp32 A
   constexpr int NB = DUAL ? 2 : 1;
-  static_assert(AV >= 1 && KR >= 2 && KR <= 8, "tile shape");
+  static_assert(KW == 1 || KW == 2, "4 or 8 waves");
+  static_assert(AV >= 1 && KR >= 1 && KR <= 8, "tile shape");
+  static_assert(KW == 1 || PD > 1, "the 8-wave schedule runs the plain pipeline");
 
   extern __shared__ __align__(16) unsigned char smem[];
   // B is staged as loaded ([k][n], pitch PB) and read with the transposing
@@ -144,7 +154,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = (wave >> 1) & 1, wn = wave & 1;
+  const int wk = wave >> 2;  // k-slice group (0 with 4 waves)
 
   // XCD-aware numbering: blocks b and b+8 run on the same XCD; give each XCD
   // a contiguous run of (split, tile) units in split-major order.
@@ -166,8 +177,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   void* Cw = CS && csel > 0 ? g.Ccol[csel - 1] : g.C;
 
   // Global-load assignment.
-  // A: vector v = tid + j*256 -> row v/8, k-chunk v%8.
-  // B: vector v = tid + r*256 -> k row v / (BN/8), column chunk v % (BN/8):
+  // A: vector v = tid + j*NTH -> row v/8, k-chunk v%8.
+  // B: vector v = tid + r*NTH -> k row v / (BN/8), column chunk v % (BN/8):
   // whole 128-byte lines per instruction.
 
   // Global loads are unconditional from clamped (always in-range)
@@ -197,7 +208,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     constexpr int P = decltype(set_tag)::value;
     const int kl = min(k0, klast);
     {
-      const int v = tid + j * kThreads;
+      const int v = tid + j * NTH;
       const int r = v >> 3, kc = (v & 7) * 8;
       const int gm = m0 + r, gk = k0 + kc;
       a_ok[P][j] = gm < g.M && gk < kend;
@@ -220,7 +231,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     const int kl = min(k0, klast);
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
-      const int v = tid + r * kThreads;
+      const int v = tid + r * NTH;
       const int kr = v / (BN / 8);
       const int gn = n0 + (v % (BN / 8)) * 8;
       const int gk = k0 + kr;
@@ -242,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     auto& a_raw_p = a_raw[P];
     auto& a_ok_p = a_ok[P];
     {
-      const int v = tid + j * kThreads;
+      const int v = tid + j * NTH;
       const int r = v >> 3, kc = (v & 7) * 8;
       float x[8];
       if constexpr (A_F32) {
@@ -321,7 +332,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         u32x4 raw = *reinterpret_cast<const u32x4*>(&b_raw_p[q][r]);
         asm volatile("" : "+v"(raw));
         if (!b_ok_p[r]) raw = u32x4{0u, 0u, 0u, 0u};
-        const int v = tid + r * kThreads;
+        const int v = tid + r * NTH;
         *reinterpret_cast<u32x4*>(Bs + ((buf * NB + q) * BK + v / (BN / 8)) * PB + (v % (BN / 8)) * 8) = raw;
       }
   };
@@ -343,7 +354,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 
   auto compute = [&](int buf) {
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
+    for (int k2 = 0; k2 < BK / 16 / KW; ++k2) {
+      const int kk = wk * (BK / 16 / KW) + k2;
       const int kof = kk * 16 + (lane >> 5) * 8;
       bf16x8 af[NA][TM];
 #pragma unroll
@@ -446,7 +458,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   __syncthreads();
   // Global loads and MFMAs per K step (for the load/MFMA interleave).
   constexpr int NLOADS = AV * AW + KR * NB;
-  constexpr int NMFMA = (BK / 16) * NB * TM * TN * NA;
+  constexpr int NMFMA = (BK / 16 / KW) * NB * TM * TN * NA;
   constexpr int MPL = NMFMA / NLOADS > 0 ? NMFMA / NLOADS : 1;
   // One K step: step s+1 goes from its register set into the buffer computed
   // on two steps ago (every wave finished reading it before the last
@@ -515,6 +527,47 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   if constexpr (PD > 2) tail(ic<1>{});
   if constexpr (PD > 3) tail(ic<2>{});
 
+  // ---- 8 waves: group 1's accumulators into group 0's, through LDS --------
+  // (the staging buffers are free: every wave passed the last step's
+  // barrier). Layout [wave of group][q][i][j][e / 4][lane] of 16-byte
+  // quads: consecutive lanes write and read consecutive quads.
+  if constexpr (KW == 2) {
+    float4* red = reinterpret_cast<float4*>(smem);
+    auto slot = [&](int q, int i, int j, int e4) {
+      return ((((wave & 3) * NB + q) * TM + i) * TN + j) * 4 * 64 + e4 * 64 + lane;
+    };
+    if (wk == 1) {
+#pragma unroll
+      for (int q = 0; q < NB; ++q)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4)
+              red[slot(q, i, j, e4)] = make_float4(acc[q][i][j][4 * e4], acc[q][i][j][4 * e4 + 1],
+                                                   acc[q][i][j][4 * e4 + 2], acc[q][i][j][4 * e4 + 3]);
+    }
+    __syncthreads();
+    if (wk == 0) {
+#pragma unroll
+      for (int q = 0; q < NB; ++q)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+              const float4 o = red[slot(q, i, j, e4)];
+              acc[q][i][j][4 * e4] += o.x;
+              acc[q][i][j][4 * e4 + 1] += o.y;
+              acc[q][i][j][4 * e4 + 2] += o.z;
+              acc[q][i][j][4 * e4 + 3] += o.w;
+            }
+    }
+    __syncthreads();  // the row sums below reuse the same LDS
+  }
+
   // ---- row sums of squares (RMSNorm epilogues) ---------------------------
   float* rs_lds = reinterpret_cast<float*>(smem);  // [BM], reuses the A buffers
   if constexpr (is_rms<EPI>()) {
@@ -524,17 +577,17 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
       v += __shfl_xor(v, 1, kWave);
       v += __shfl_xor(v, 2, kWave);
       v += __shfl_xor(v, 4, kWave);
-      sq[j] = v;  // row (tid + j*256)/8, identical across its 8 threads
+      sq[j] = v;  // row (tid + j*NTH)/8, identical across its 8 threads
     }
     if (g.S == 1) {
 #pragma unroll
       for (int j = 0; j < AV; ++j)
-        if ((tid & 7) == 0) rs_lds[(tid + j * kThreads) >> 3] = sq[j];
+        if ((tid & 7) == 0) rs_lds[(tid + j * NTH) >> 3] = sq[j];
       __syncthreads();
     } else {
 #pragma unroll
       for (int j = 0; j < AV; ++j) {
-        const int r = (tid + j * kThreads) >> 3;
+        const int r = (tid + j * NTH) >> 3;
         // Every N tile computes the same row sums; the first one publishes.
         if ((tid & 7) == 0 && m0 + r < g.M && nt == 0)
           g.rowsq[(static_cast<int64_t>(z) * g.NT + nt) * g.M + m0 + r] = sq[j];
@@ -567,6 +620,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
       else static_cast<bf16*>(Cw)[o] = static_cast<bf16>(v0);
     }
   };
+
+  // With 8 waves group 0 holds the sums and writes the outputs.
+  if (KW == 2 && wk != 0) return;
 
   if (g.S == 1) {
 #pragma unroll
@@ -1108,7 +1164,16 @@ size_t lds_bytes(int BM, int BN, int na, int nb) {
 // static allocation of the kernel).
 constexpr size_t kMaxLds = 160 * 1024 - 256;
 
-int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, std::string* why) {
+// gemm_kernel's dynamic LDS: the staging buffers, and with 8 waves at least
+// the fp32 accumulators of 4 waves (the k-slice groups' sum).
+size_t gemm_lds_bytes(int BM, int BN, int na, int nb, int threads) {
+  const size_t stage = lds_bytes(BM, BN, na, nb);
+  const size_t red = threads > kThreads ? static_cast<size_t>(nb) * BM * BN * sizeof(float) : 0;
+  return stage > red ? stage : red;
+}
+
+int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, std::string* why,
+                     int threads = kThreads) {
   if (M < 0 || N < 0 || K < 0 || M > (1 << 30) || N > (1 << 30) || K > (1 << 30)) {
     *why = "dimension out of range";
     return AXON_EINVAL;
@@ -1132,7 +1197,7 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, st
     return AXON_EINVAL;
   }
   const Plan p = plan_of(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), tm, tn, tk);
-  if (!grid_fits(static_cast<int64_t>(p.S) * p.MT * p.NT, 1, kThreads) ||
+  if (!grid_fits(static_cast<int64_t>(p.S) * p.MT * p.NT, 1, threads) ||
       (p.S > 1 && !grid_fits((M * N / 4 + 255) / 256, 1, 256))) {
     *why = "grid too large for one dispatch (fewer than 2^32 work-items)";
     return AXON_EINVAL;
@@ -1156,11 +1221,11 @@ size_t gemm_workspace(int M, int N, int K, int tm, int tn, int tk, int nb) {
   return data_bytes(p, M, N, nb);
 }
 
-template <int BM, int BN, int EPI, bool AF, int PD>
+template <int BM, int BN, int EPI, bool AF, int PD, int NTH = kThreads>
 void launch_tile(const GemmArgs& g, hipStream_t st) {
   constexpr int na = AF ? 2 : 1, nb = EPI == kSiluMul ? 2 : 1;
-  const size_t lds = lds_bytes(BM, BN, na, nb);
-  auto fn = gemm_kernel<BM, BN, EPI, AF, PD>;
+  const size_t lds = gemm_lds_bytes(BM, BN, na, nb, NTH);
+  auto fn = gemm_kernel<BM, BN, EPI, AF, PD, NTH>;
   // Raising the dynamic LDS limit is idempotent, so a race between threads
   // doing it for the first time is harmless.
   static std::atomic<bool> configured{false};
@@ -1171,7 +1236,7 @@ void launch_tile(const GemmArgs& g, hipStream_t st) {
   }
   const unsigned blocks = static_cast<unsigned>(g.S * g.MT * g.NT);
   if (blocks == 0) return;  // an empty output (m or n is 0 inside a composite)
-  hipLaunchKernelGGL(fn, dim3(blocks), dim3(kThreads), lds, st, g);
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(NTH), lds, st, g);
   if (g.S > 1) {
     const int64_t quads = static_cast<int64_t>(g.M) * g.N / 4;
     hipLaunchKernelGGL(splitk_reduce_kernel<EPI>, dim3(static_cast<unsigned>((quads + 255) / 256)),
@@ -1210,8 +1275,8 @@ void launch_dma_tile(const GemmArgs& g, hipStream_t st) {
 
 // One GEMM launch's grids (the main kernel and, with split K, the fixup) fit
 // one dispatch each.
-int gemm_grid_check(const GemmArgs& g) {
-  int rc = grid_check("gemm_kernel", static_cast<int64_t>(g.S) * g.MT * g.NT, 1, kThreads);
+int gemm_grid_check(const GemmArgs& g, int threads = kThreads) {
+  int rc = grid_check("gemm_kernel", static_cast<int64_t>(g.S) * g.MT * g.NT, 1, threads);
   if (rc == AXON_OK && g.S > 1)
     rc = grid_check("splitk_reduce_kernel", (static_cast<int64_t>(g.M) * g.N / 4 + 255) / 256, 1, 256);
   return rc;
@@ -1238,6 +1303,41 @@ int dispatch_dma(int BM, int BN, const GemmArgs& g, hipStream_t st) {
 
 // Prefetch depth of hw variant 1 (register sets of loads in flight).
 constexpr int deep_pd(int BM, int BN) { return BM * BN <= 128 * 128 ? 3 : 2; }
+
+// 8-wave workgroups (hw variant 3 of the plain GEMMs, 2 of the RMSNorm
+// GEMMs): the schedule of hw variant 1 with a second group of 4 waves on the
+// other half of every K step's k-slices, each thread loading half as much
+// per K step, and 4 (up to 128 x 128) or 2 K steps of loads in flight. A CU
+// takes in its L2 lines faster with 8 waves issuing loads than with 4 (the
+// skinny GEMM's load stream alone: 23.9 us with 4 waves, 18.6 us with 8 at
+// 4 steps in flight), and each SIMD has a second wave to issue while the
+// other waits for its fragments. 256 x 256 tiles are left out: two waves of
+// 128 accumulator registers each per SIMD leave too few for the staging.
+constexpr int kWideThreads = 512;
+constexpr int wide_pd(int BM, int BN) { return BM * BN <= 128 * 128 ? 4 : 2; }
+
+bool wide_tile_ok(int tm, int tn) { return tile_ok(tm, tn) && tm * tn < 16; }
+
+template <int EPI>
+int dispatch_wide(int BM, int BN, const GemmArgs& g, hipStream_t st) {
+  if (const int rc = gemm_grid_check(g, kWideThreads); rc != AXON_OK) return rc;
+#define AXON_GEMM_CASE(bm, bn)                                                       \
+  if (BM == bm && BN == bn) {                                                        \
+    launch_tile<bm, bn, EPI, false, wide_pd(bm, bn), kWideThreads>(g, st);           \
+    return launch_status("gemm_kernel");                                             \
+  }
+  AXON_GEMM_CASE(64, 64)
+  AXON_GEMM_CASE(64, 128)
+  AXON_GEMM_CASE(64, 256)
+  AXON_GEMM_CASE(128, 64)
+  AXON_GEMM_CASE(128, 128)
+  AXON_GEMM_CASE(128, 256)
+  AXON_GEMM_CASE(256, 64)
+  AXON_GEMM_CASE(256, 128)
+#undef AXON_GEMM_CASE
+  set_error("no 8-wave GEMM instantiation for this tile");
+  return AXON_EINVAL;
+}
 
 template <int EPI, bool AF>
 int dispatch(int BM, int BN, const GemmArgs& g, hipStream_t st, int variant = 0) {
@@ -1342,7 +1442,15 @@ int check_mm(const Call& c, std::string* why) {
     *why = "bf16 inputs only";
     return AXON_EDTYPE;
   }
-  return check_gemm_shape(c.dim(0), c.dim(1), c.dim(2), c.tile(0), c.tile(1), c.tile(2), why);
+  // softmax_mm (two hw variants) has no 8-wave schedule.
+  const bool wide = EPI != kSoftmax && c.variant == 2;
+  if (wide && !wide_tile_ok(c.tile(0), c.tile(1))) {
+    *why = "8-wave tiles go up to 256 x 128: TILES_IN_BLOCK_M/N each 1, 2 or 4 with a "
+           "product below 16";
+    return AXON_EINVAL;
+  }
+  return check_gemm_shape(c.dim(0), c.dim(1), c.dim(2), c.tile(0), c.tile(1), c.tile(2), why,
+                          wide ? kWideThreads : kThreads);
 }
 
 // Manifest extent of TILES_IN_BLOCK_K for a contraction of length K: the
@@ -1414,8 +1522,20 @@ int manifest_splitk(int v, const int64_t* dims, int dt, Constraint* out, int cap
 }
 
 // The plain matmul families have a third hw variant (direct-to-LDS loads)
-// that needs whole 64-deep K steps.
+// that needs whole 64-deep K steps, and a fourth with 8-wave workgroups;
+// the RMSNorm GEMMs have the 8-wave schedule as their third.
 constexpr int kDmaVariant = 2;
+template <int EPI>
+constexpr int wide_variant() { return EPI == kPlain ? 3 : 2; }
+
+int check_wide_tile(const Call& c, std::string* why) {
+  if (!wide_tile_ok(c.tile(0), c.tile(1))) {
+    *why = "8-wave tiles go up to 256 x 128: TILES_IN_BLOCK_M/N each 1, 2 or 4 with a "
+           "product below 16";
+    return AXON_EINVAL;
+  }
+  return AXON_OK;
+}
 
 // fp32 inputs (hw variants 0 and 1): a prep pass splits x into bf16 rows
 // [hi | lo | hi] and w into planes [hi; hi; lo], and the bf16 GEMM over
@@ -1434,8 +1554,8 @@ int check_plain(const Call& c, std::string* why) {
     return AXON_EDTYPE;
   }
   if (dt == AXON_F32) {
-    if (c.variant == kDmaVariant) {
-      *why = "hw variant 2 has no fp32 instantiation; fp32 inputs use hw variants 0 and 1";
+    if (c.variant == kDmaVariant || c.variant == wide_variant<kPlain>()) {
+      *why = "hw variants 2 and 3 have no fp32 instantiation; fp32 inputs use hw variants 0 and 1";
       return AXON_EDTYPE;
     }
     if (c.dim(2) % 8 != 0 || c.dim(2) > (1 << 28)) {
@@ -1443,8 +1563,13 @@ int check_plain(const Call& c, std::string* why) {
       return AXON_EINVAL;
     }
   }
+  const bool wide = c.variant == wide_variant<kPlain>();
+  if (wide) {
+    const int rc = check_wide_tile(c, why);
+    if (rc != AXON_OK) return rc;
+  }
   const int rc = check_gemm_shape(c.dim(0), c.dim(1), plain_kp(c.dim(2), dt), c.tile(0), c.tile(1),
-                                  c.tile(2), why);
+                                  c.tile(2), why, wide ? kWideThreads : kThreads);
   if (rc != AXON_OK) return rc;
   if (c.variant == kDmaVariant && c.dim(2) % BK != 0) {
     *why = "hw variant 2 loads whole 64-deep K steps: k must be a multiple of 64";
@@ -1456,7 +1581,7 @@ int check_plain(const Call& c, std::string* why) {
 int manifest_plain(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   const int64_t mnk[3] = {dims[0], dims[1], dt == AXON_F32 ? 3 * dims[2] : dims[2]};
   const int n = manifest_splitk(v, mnk, dt, out, cap);
-  if (v == kDmaVariant && (dims[2] % BK != 0 || dt == AXON_F32))
+  if ((v == kDmaVariant && (dims[2] % BK != 0 || dt == AXON_F32)) || (v == wide_variant<kPlain>() && dt == AXON_F32))
     for (int i = 0; i < n; ++i) out[i].extent = 0;  // admits no tile
   return n;
 }
@@ -1542,10 +1667,26 @@ int launch_mm(const Call& c, const void* const* in, void* const* out, void* ws, 
   if constexpr (EPI == kPlain) {
     if (c.variant == kDmaVariant) return dispatch_dma<kPlain>(p.BM, p.BN, g, st);
   }
+  if constexpr (EPI == kPlain || EPI == kRmsSum || EPI == kRmsEps) {
+    if (c.variant == wide_variant<EPI>()) return dispatch_wide<EPI>(p.BM, p.BN, g, st);
+  }
   return dispatch<EPI, false>(p.BM, p.BN, g, st, c.variant);
 }
 
+const char* summary_wide() {
+  return "bf16 MFMA 32x32x16, 8 waves per BMxBN tile (two groups of 2x2 waves on the two halves of "
+         "every K step's k-slices, summed through LDS at the end), 4 K steps (2 above 128x128 tiles) "
+         "of global loads in flight in rotating register sets, LDS double "
+         "buffer with B staged as loaded and read by the transposing LDS read, split-K with a parallel "
+         "fixup kernel, XCD-grouped K ranges, fused row-scale epilogue";
+}
+
+// RMSNorm GEMMs: hw variants 0 and 1 as the plain GEMM's, 2 = 8-wave.
+const char* summary_mm(int variant);
+const char* summary_rms(int variant) { return variant == 2 ? summary_wide() : summary_mm(variant); }
+
 const char* summary_mm(int variant) {
+  if (variant == 3) return summary_wide();
   if (variant == kDmaVariant)
     return "bf16 MFMA 32x32x16, 4 waves per BMxBN tile, A and B tiles loaded straight into LDS "
            "(global_load_lds_dwordx4, chunk-swizzled stages, up to 4 stages = 3 K steps in flight), "
@@ -2196,15 +2337,15 @@ const char* summary_attn_qkv(int variant) {
 
 #define AXON_MM_FAMILY(fn_name, spec_name, EPI)                                                \
   const Family* fn_name() {                                                                  \
-    static const Family f = {spec_name,     2,           2,         1,           3,          \
-                             kTileArgs3,    3,           summary_mm, manifest_splitk, check_mm<EPI>, \
+    static const Family f = {spec_name,     3,           2,         1,           3,          \
+                             kTileArgs3,    3,           summary_rms, manifest_splitk, check_mm<EPI>, \
                              workspace_mm<EPI>, outputs_mm, launch_mm<EPI>};                  \
     return &f;                                                                               \
   }
 
 #define AXON_PLAIN_FAMILY(fn_name, spec_name)                                                    \
   const Family* fn_name() {                                                                    \
-    static const Family f = {spec_name,     3,          2,              1,           3,        \
+    static const Family f = {spec_name,     4,          2,              1,           3,        \
                              kTileArgs3,    3,          summary_mm,     manifest_plain, check_plain, \
                              workspace_plain, outputs_mm, launch_plain};                         \
     return &f;                                                                                 \

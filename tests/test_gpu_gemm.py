@@ -52,7 +52,7 @@ def test_gemm_parity(name, sizes):
     assert check_parity(name, sizes, rtol=1e-2, atol=1e-2, budget=10)
 
 
-@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("variant", [0, 1, 3])
 def test_gemm_repeated_launches_bit_identical(variant):
     """Split-K launches reuse one workspace: ten launches give the same bits
     every time (the fixup sums the partials in a fixed order)."""
