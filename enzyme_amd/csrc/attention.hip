@@ -63,6 +63,7 @@ constexpr int KP = D + 8;  // Ks row pitch (elements): 16-byte reads of 8 rows h
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.f;  // log2 of the largest un-rescaled probability
 constexpr int kXcds = 8;
+constexpr int kMaxSplits = 16;  // key ranges of hw variant 3
 
 template <int N>
 using ic = std::integral_constant<int, N>;
@@ -667,9 +668,9 @@ __global__ __launch_bounds__(W * 64, W == 4 ? 2 : 1) void attn_sp_kernel(AttnArg
 // Merges the key ranges of hw variant 3, one wave per query row (two of
 // the 128 output columns per lane): with M the largest running max,
 // O = sum_r 2^(m_r - M) O_r / sum_r 2^(m_r - M) l_r. Lane r < nsplit loads
-// range r's (max, sum) pair, so the weights take one load and two wave
-// reductions; the output columns of the ranges are then loaded four at a
-// time.
+// range r's (max, sum) pair, and every range's two output columns are
+// loaded in the same round, before the weights are formed, so a row costs
+// one memory round trip; the weights then take two wave reductions.
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ o_part,
                                                            const float* __restrict__ ml_part,
                                                            bf16* __restrict__ o, int nsplit,
@@ -679,17 +680,21 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const int lane = threadIdx.x & 63;
   float2 ml = make_float2(-INFINITY, 0.f);
   if (lane < nsplit) ml = *reinterpret_cast<const float2*>(ml_part + (lane * rows + row) * 2);
+  float2 v[kMaxSplits];
+#pragma unroll
+  for (int r = 0; r < kMaxSplits; ++r)
+    if (r < nsplit) v[r] = *reinterpret_cast<const float2*>(o_part + (r * rows + row) * D + 2 * lane);
   const float mx = wave_max(ml.x);
   const float w = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
   const float l = wave_sum(w * ml.y);
   float o0 = 0.f, o1 = 0.f;
-#pragma unroll 4
-  for (int r = 0; r < nsplit; ++r) {
-    const float wr = __shfl(w, r, 64);
-    const float2 v = *reinterpret_cast<const float2*>(o_part + (r * rows + row) * D + 2 * lane);
-    o0 += wr * v.x;
-    o1 += wr * v.y;
-  }
+#pragma unroll
+  for (int r = 0; r < kMaxSplits; ++r)
+    if (r < nsplit) {
+      const float wr = __shfl(w, r, 64);
+      o0 += wr * v[r].x;
+      o1 += wr * v[r].y;
+    }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   bf16 out[2] = {static_cast<bf16>(o0 * inv), static_cast<bf16>(o1 * inv)};
   *reinterpret_cast<uint32_t*>(o + row * D + 2 * lane) = pack2(out[0], out[1]);
@@ -723,7 +728,6 @@ AttnTiles attn_tiles(const Call& c) {
 // rows (batch * heads * s), where the other variants cannot fill the GPU and
 // its workspace (nsplit * rows * 520 bytes) stays below 136 MB.
 constexpr int64_t kSplitMaxRows = 16384;
-constexpr int kMaxSplits = 16;
 
 int check_split_tiles(const Call& c, int64_t rows, std::string* why) {
   const int tm = c.tile(0), TN = c.tile(1), ns = c.tile(2);
