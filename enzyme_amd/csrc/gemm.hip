@@ -1578,9 +1578,23 @@ int check_plain(const Call& c, std::string* why) {
   return AXON_OK;
 }
 
+// The 8-wave schedule stops at 256 x 128 tiles: its manifest caps BN at 128
+// so the box never admits 256 x 256 (128 x 256 and 64 x 256 stay legal,
+// reachable with the candidate filter off).
+void cap_wide(Constraint* out, int n) {
+  if (n >= 2) out[1].extent = std::min<int64_t>(out[1].extent, 128);
+}
+
+int manifest_rms(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
+  const int n = manifest_splitk(v, dims, dt, out, cap);
+  if (v == wide_variant<kRmsEps>()) cap_wide(out, n);
+  return n;
+}
+
 int manifest_plain(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   const int64_t mnk[3] = {dims[0], dims[1], dt == AXON_F32 ? 3 * dims[2] : dims[2]};
   const int n = manifest_splitk(v, mnk, dt, out, cap);
+  if (v == wide_variant<kPlain>()) cap_wide(out, n);
   if ((v == kDmaVariant && (dims[2] % BK != 0 || dt == AXON_F32)) || (v == wide_variant<kPlain>() && dt == AXON_F32))
     for (int i = 0; i < n; ++i) out[i].extent = 0;  // admits no tile
   return n;
@@ -2338,7 +2352,7 @@ const char* summary_attn_qkv(int variant) {
 #define AXON_MM_FAMILY(fn_name, spec_name, EPI)                                                \
   const Family* fn_name() {                                                                  \
     static const Family f = {spec_name,     3,           2,         1,           3,          \
-                             kTileArgs3,    3,           summary_rms, manifest_splitk, check_mm<EPI>, \
+                             kTileArgs3,    3,           summary_rms, manifest_rms, check_mm<EPI>,    \
                              workspace_mm<EPI>, outputs_mm, launch_mm<EPI>};                  \
     return &f;                                                                               \
   }

@@ -204,6 +204,24 @@ def test_manifest_admits_only_legal_tiles():
     assert checked > 500
 
 
+@pytest.mark.parametrize(("name", "dims"), [("matmul", [4096, 4096, 4096]), ("matmul_std002", [8192, 8192, 1024]),
+                                          ("rmsnorm_matmul", [4096, 4096, 4096]),
+                                          ("rmsnorm_matmul_eps", [8192, 8192, 1024])])
+def test_manifest_admits_only_legal_tiles_at_large_outputs(name, dims):
+    """Shapes whose occupancy box reaches 256 x 256 tiles: the 8-wave hw
+    variant (up to 256 x 128) must still admit only tuples it accepts."""
+    from axon.candidate_filter import rejection_reason
+
+    spec = load_spec(name)
+    codes = [hip.AXON_BF16] * len(spec.input_specs)
+    for v in range(hip.variant_count(name)):
+        cons = hip.manifest(name, v, dims, codes[0])
+        for t in product(spec.tile_options, repeat=len(spec.tile_args)):
+            if rejection_reason(spec.tile_args, t, cons) is None:
+                st, why = hip.check(name, v, t, dims, codes)
+                assert st == hip.AXON_OK, (name, v, t, why)
+
+
 # Small legal dims per spec; the first dim is set to 0 below.
 _EMPTY_DIMS = {"attention_causal": [1, 2, 64, 128], "attention_nkilib": [64, 128],
                "rope_llama3": [1, 64, 4, 2, 128], "rope": [64, 128]}
