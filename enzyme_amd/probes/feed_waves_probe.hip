@@ -10,7 +10,9 @@
 // Build and run (repository root):
 //   hipcc --offload-arch=gfx950 -O3 -Xclang -target-feature -Xclang -packed-fp32-ops \
 //       enzyme_amd/probes/feed_waves_probe.hip -o enzyme_amd/probes/_build/feed_waves_probe
-//   enzyme_amd/probes/_build/feed_waves_probe
+//   enzyme_amd/probes/_build/feed_waves_probe [reps [first_case last_case]]
+// With arguments (for counter runs): reps timed and reps untimed launches per
+// case, and only cases first_case..last_case (0-11, in the order printed).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -146,8 +148,12 @@ __global__ __launch_bounds__(NT) void gemm_loads(const unsigned short* __restric
   if (acc.x == 0x12345678u && acc.y == 0x9abcdefu) sink[blockIdx.x] = acc;
 }
 
+int g_reps = 200, g_warm = 300, g_first = 0, g_last = 1 << 30, g_case = 0;
+
 template <int BM, int BN, int NT, int PD>
 int gemm_case(const Shape& sh) {
+  const int idx = g_case++;
+  if (idx < g_first || idx > g_last) return 0;
   const size_t abytes = static_cast<size_t>(sh.M) * sh.K * 2, bbytes = static_cast<size_t>(sh.K) * sh.N * 2;
   const int nsets = static_cast<int>(std::max<size_t>(1, std::min<size_t>(64, ((1ull << 30) + abytes + bbytes - 1) / (abytes + bbytes))));
   std::vector<unsigned short*> as(nsets), bs(nsets);
@@ -163,7 +169,7 @@ int gemm_case(const Shape& sh) {
   hipEvent_t a, b;
   CK(hipEventCreate(&a));
   CK(hipEventCreate(&b));
-  const int warm = 300, reps = 200;
+  const int warm = g_warm, reps = g_reps;
   for (int w = 0; w < warm; ++w)
     hipLaunchKernelGGL((gemm_loads<BM, BN, NT, PD>), dim3(G), dim3(NT), 0, 0, as[w % nsets], bs[w % nsets], sink, sh);
   CK(hipGetLastError());
@@ -176,8 +182,8 @@ int gemm_case(const Shape& sh) {
   CK(hipEventElapsedTime(&ms, a, b));
   const double us = ms * 1e3 / reps;
   const double cu_bytes = static_cast<double>(G) * (static_cast<double>(BM) + BN) * sh.krange * 2.0;
-  std::printf("gemm %dx%dx%d tiles %dx%d Krange %d G %d threads %d PD %d: %.2f us  %.1f B/clk/CU\n",
-              sh.M, sh.N, sh.K, BM, BN, sh.krange, G, NT, PD, us, cu_bytes / (us * 1e-6) / kClockHz / kCus);
+  std::printf("case %d gemm %dx%dx%d tiles %dx%d Krange %d G %d threads %d PD %d: %.2f us  %.1f B/clk/CU\n",
+              idx, sh.M, sh.N, sh.K, BM, BN, sh.krange, G, NT, PD, us, cu_bytes / (us * 1e-6) / kClockHz / kCus);
   for (int i = 0; i < nsets; ++i) {
     CK(hipFree(as[i]));
     CK(hipFree(bs[i]));
@@ -188,7 +194,12 @@ int gemm_case(const Shape& sh) {
 
 }  // namespace
 
-int main() {
+int main(int argc, char** argv) {
+  if (argc > 1) g_reps = g_warm = std::max(1, std::atoi(argv[1]));
+  if (argc > 3) {
+    g_first = std::atoi(argv[2]);
+    g_last = std::atoi(argv[3]);
+  }
   Shape sh;
   sh.M = 1024; sh.N = 512; sh.K = 16384; sh.BM = 128; sh.BN = 128; sh.krange = 2048;
   sh.MT = sh.M / sh.BM; sh.NT = sh.N / sh.BN; sh.S = sh.K / sh.krange;
