@@ -105,7 +105,7 @@ CONFIGS = [
         label="causal attention Q/K/V [1,32,4096,128] bf16, scale 1/sqrt(128)",
     ),
     dict(
-        spec="qkv_cte", sizes=(16384, 512, 8192), variant=2, tiles=(4, 4, 16), bound="hbm",
+        spec="qkv_cte", sizes=(16384, 512, 8192), variant=3, tiles=(2, 2, 16), bound="hbm",
         work=3 * 16384 * 8192 * 2 + 8192 * 512 * 2 + 16384 * 512 * 2, flops=2 * 16384 * 512 * 8192,
         rtol=2e-2, atol=2e-2,
         label="qkv_cte llama70b: x, mlp_prev, attention_prev [16384,8192] bf16 summed, RMSNorm eps 1e-6, "

@@ -1128,6 +1128,253 @@ __global__ __launch_bounds__(256) void split_rows_hilo_kernel(const float* __res
 }
 
 // ---------------------------------------------------------------------------
+// hw variant 3 of qkv_cte (bf16): full-width N tiles with the B operand
+// loaded straight into registers.
+//
+// One workgroup per BM x BN output tile and K range, BN = 64 x waves, so at
+// n = 512 one N tile covers every column and each residual row leaves memory
+// once per K range. hw variant 2's 256 x 256 tiles read every A row twice,
+// once per N tile. Replayed as loads only (A rows plus the B block, 8 waves),
+// the two patterns take 227 and 155 us at 16384 x 512 x 8192. Wave w owns the
+// output columns 64 w .. 64 w + 63 of the tile and all BM rows:
+//   * A, h = (x + mlp_prev) + attention_prev (summed in fp32, squares summed
+//     for the row scale, rounded to bf16), is staged once per K step in LDS
+//     and read by every wave;
+//   * B goes from memory straight into the MFMA operand registers. A pre-pass
+//     (qkv_pack_w_kernel) lays w out so that each 16-deep slice of a
+//     32-column tile is one contiguous KiB holding the 64 lanes' operands in
+//     lane order: every B load instruction of a wave reads one whole KiB, and
+//     no B byte passes through LDS.
+// k order inside a 64-deep step: slice kk of lane half h (lane / 32) holds
+// k = 32 h + 8 kk + (0..7). A is read from LDS at that offset and B is packed
+// the same way, so each MFMA slice sums over a fixed k set and the four
+// slices together cover the step's 64 k values once.
+// ---------------------------------------------------------------------------
+constexpr int kPackCols = 256;              // columns of w per pre-pass workgroup
+constexpr int kPackPitch = kPackCols + 8;   // LDS row pitch (elements), 16-byte aligned rows
+
+// w [K, N] bf16 -> fragments: fragment ((s * nct + ct) * 4 + kk) * 64 + l
+// (16 bytes) holds w[k][n] for n = 32 ct + l % 32 and
+// k = 64 s + 32 (l / 32) + 8 kk + (0..7); k >= K or n >= N read as 0.
+// Grid (Kp / 64, Np / 256): workgroup (s, cg) reads the 64 x 256 block with
+// 16-byte row loads into LDS, then writes its 2048 fragments (one
+// contiguous 32 KiB run) with each thread gathering 8 rows of one column.
+__global__ __launch_bounds__(256) void qkv_pack_w_kernel(const bf16* __restrict__ w, u32x4* __restrict__ out,
+                                                         int K, int N, int nct) {
+  __shared__ __align__(16) bf16 tile[64 * kPackPitch];
+  const int s = blockIdx.x, cg = blockIdx.y;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int v = tid + i * 256;  // 64 rows x 32 vectors of 8 columns
+    const int r = v >> 5, c8 = v & 31;
+    const int k = s * 64 + r, n = cg * kPackCols + c8 * 8;
+    u32x4 val = {0u, 0u, 0u, 0u};
+    if (k < K && n < N) val = *reinterpret_cast<const u32x4*>(w + static_cast<int64_t>(k) * N + n);  // N % 8 == 0
+    *reinterpret_cast<u32x4*>(tile + r * kPackPitch + c8 * 8) = val;
+  }
+  __syncthreads();
+  u32x4* dst = out + (static_cast<int64_t>(s) * nct + cg * (kPackCols / 32)) * 256;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int f = tid + i * 256;  // (column tile, slice, lane) = (f / 256, f / 64 % 4, f % 64)
+    const int l = f & 63, kk = (f >> 6) & 3;
+    const int col = (f >> 8) * 32 + (l & 31);
+    const int k0 = 32 * (l >> 5) + 8 * kk;
+    bf16x8 frag;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) frag[e] = tile[(k0 + e) * kPackPitch + col];
+    dst[f] = __builtin_bit_cast(u32x4, frag);
+  }
+}
+
+template <int BM, int NW>
+__global__ __launch_bounds__(64 * NW) void qkv_wide_kernel(GemmArgs g, const u32x4* __restrict__ wp, int nct) {
+  constexpr int NTH = 64 * NW, BN = 64 * NW;
+  constexpr int TM = BM / 32;        // 32-row MFMA tiles of a wave
+  constexpr int AV = BM * 8 / NTH;   // A vectors (8 k values of one row) per thread per step
+  static_assert(AV >= 1 && (BM * 8) % NTH == 0, "tile shape");
+  __shared__ __align__(16) bf16 As[2 * BM * LDK];
+  __shared__ float rs[BM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  const int G = g.S * g.MT * g.NT;
+  int unit = blockIdx.x;
+  if (G % kXcds == 0) unit = (blockIdx.x % kXcds) * (G / kXcds) + blockIdx.x / kXcds;
+  const int z = unit / (g.MT * g.NT);
+  const int tile = unit - z * g.MT * g.NT;
+  const int mt = tile / g.NT, nt = tile - mt * g.NT;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int kbeg = z * g.kchunk;
+  const int kend = min(g.K, kbeg + g.kchunk);
+  const int nsteps = max(0, (kend - kbeg + BK - 1) / BK);
+  // Loads past the K range re-read its last step (never used): branch-free.
+  const int klast = kbeg + max(nsteps - 1, 0) * BK;
+
+  const bf16* X = static_cast<const bf16*>(g.A);
+  // A: vector v = tid + j * NTH -> row v / 8, k chunk v % 8 (8 lanes read one
+  // row's 128 bytes of a step).
+  Vec<bf16> araw[AV][3];
+  bool aok[AV];
+  float sq[AV];
+#pragma unroll
+  for (int j = 0; j < AV; ++j) sq[j] = 0.f;
+  auto load_a = [&](int k0) __attribute__((always_inline)) {
+    const int kl = min(k0, klast);
+#pragma unroll
+    for (int j = 0; j < AV; ++j) {
+      const int v = tid + j * NTH;
+      const int r = v >> 3, kc = (v & 7) * 8;
+      const int gm = m0 + r;
+      aok[j] = gm < g.M && k0 + kc < kend;
+      const int64_t off = static_cast<int64_t>(min(gm, g.M - 1)) * g.K + min(kl + kc, g.K - 8);
+      araw[j][0] = load_vec_nt(X + off);
+      araw[j][1] = load_vec_nt(g.A2 + off);
+      araw[j][2] = load_vec_nt(g.A3 + off);
+    }
+  };
+  auto store_a = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < AV; ++j) {
+      const int v = tid + j * NTH;
+      const int r = v >> 3, kc = (v & 7) * 8;
+      Vec<bf16> t;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float h = (to_f32(araw[j][0].v[e]) + to_f32(araw[j][1].v[e])) + to_f32(araw[j][2].v[e]);
+        const float x = aok[j] ? h : 0.f;
+        sq[j] += x * x;
+        t.v[e] = static_cast<bf16>(x);
+      }
+      store_vec(As + (buf * BM + r) * LDK + kc, t);
+    }
+  };
+
+  // B fragments of this wave's two 32-column tiles, one per 16-deep slice.
+  u32x4 bfr[2][4];
+  const u32x4* wcol = wp + static_cast<int64_t>(n0 / 32 + 2 * wave) * 256 + lane;
+  auto load_b = [&](int s, int j, int kk) __attribute__((always_inline)) {
+    const int sg = min(kbeg + s * BK, klast) / BK;
+    bfr[j][kk] = wcol[(static_cast<int64_t>(sg) * nct + j) * 256 + kk * 64];
+  };
+
+  floatx16 acc[TM][2];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  bf16x8 af[2][TM];
+  auto read_a = [&](int buf, int kk, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      af[slot][i] = *reinterpret_cast<const bf16x8*>(As + (buf * BM + 32 * i + (lane & 31)) * LDK + 32 * (lane >> 5) +
+                                                     8 * kk);
+  };
+
+  // Step s: its A tile in LDS buffer s % 2 and its B fragments in bfr. Each
+  // slice's MFMAs are followed by the reload of that slice's B fragments for
+  // step s + 1; after slice 1 the next step's A vectors (loaded one step
+  // earlier) are summed into the other buffer and step s + 2's are loaded.
+  // One barrier per step: it publishes the A tile of step s + 1 and retires
+  // every read of the buffer the following step overwrites.
+  if (nsteps > 0) {
+    load_a(kbeg);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) load_b(0, j, kk);
+    store_a(0);
+    load_a(kbeg + BK);
+    __syncthreads();
+    for (int s = 0; s < nsteps; ++s) {
+      const int buf = s & 1;
+      read_a(buf, 0, 0);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        if (kk + 1 < 4) read_a(buf, kk + 1, (kk + 1) & 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][i], __builtin_bit_cast(bf16x8, bfr[j][kk]),
+                                                                acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) load_b(s + 1, j, kk);
+        if (kk == 1) {
+          store_a(buf ^ 1);
+          load_a(kbeg + (s + 2) * BK);
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // Row sums of squares: row (tid + j * NTH) / 8 is spread over 8 lanes.
+#pragma unroll
+  for (int j = 0; j < AV; ++j) {
+    float v = sq[j];
+    v += __shfl_xor(v, 1, kWave);
+    v += __shfl_xor(v, 2, kWave);
+    v += __shfl_xor(v, 4, kWave);
+    sq[j] = v;
+  }
+  // Accumulator element e of MFMA tile (i, j): row 32 i + 8 (e / 4) +
+  // 4 (lane / 32) + e % 4, column 64 wave + 32 j + lane % 32.
+  auto row_of = [&](int i, int e) { return i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); };
+  auto col_of = [&](int j) { return wave * 64 + j * 32 + (lane & 31); };
+
+  if (g.S == 1) {
+#pragma unroll
+    for (int j = 0; j < AV; ++j)
+      if ((tid & 7) == 0) rs[(tid + j * NTH) >> 3] = sq[j];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = row_of(i, e);
+        const int gm = m0 + r;
+        if (gm >= g.M) continue;
+        // An empty contraction has zero accumulators and an empty row: 0.
+        const float sc = g.K == 0 ? 0.f : 1.f / sqrtf(rs[r] / static_cast<float>(g.K) + g.eps);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int gn = n0 + col_of(j);
+          if (gn < g.N) static_cast<bf16*>(g.C)[static_cast<int64_t>(gm) * g.N + gn] = static_cast<bf16>(acc[i][j][e] * sc);
+        }
+      }
+    return;
+  }
+  // Split K: the partial tile and (first N tile only) the row sums; the
+  // splitk_reduce_kernel<kQkv> fixup sums both over the splits.
+#pragma unroll
+  for (int j = 0; j < AV; ++j) {
+    const int r = (tid + j * NTH) >> 3;
+    if ((tid & 7) == 0 && m0 + r < g.M && nt == 0) g.rowsq[(static_cast<int64_t>(z) * g.NT + nt) * g.M + m0 + r] = sq[j];
+  }
+  const int64_t MN = static_cast<int64_t>(g.M) * g.N;
+  float* dst = g.partial + static_cast<int64_t>(z) * MN;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int gm = m0 + row_of(i, e);
+      if (gm >= g.M) continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int gn = n0 + col_of(j);
+        if (gn < g.N) dst[static_cast<int64_t>(gm) * g.N + gn] = acc[i][j][e];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 const char* const kTileArgs3[] = {"TILES_IN_BLOCK_M", "TILES_IN_BLOCK_N", "TILES_IN_BLOCK_K"};
@@ -1172,8 +1419,14 @@ size_t gemm_lds_bytes(int BM, int BN, int na, int nb, int threads) {
   return stage > red ? stage : red;
 }
 
+// qkv_cte hw variant 3 counts its tiles differently: TILES_IN_BLOCK_M = BM / 64
+// (1 or 2) and TILES_IN_BLOCK_N = BN / 256 (1 or 2: 256 or 512 columns, one
+// wave per 64), so its manifest box is exactly its legal set.
+bool qkv_wide_tile_ok(int tm, int tn) { return (tm == 1 || tm == 2) && (tn == 1 || tn == 2); }
+constexpr int kQkvWideCols = 256;  // columns per TILES_IN_BLOCK_N of hw variant 3
+
 int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, std::string* why,
-                     int threads = kThreads) {
+                     int threads = kThreads, bool qkv_wide = false) {
   if (M < 0 || N < 0 || K < 0 || M > (1 << 30) || N > (1 << 30) || K > (1 << 30)) {
     *why = "dimension out of range";
     return AXON_EINVAL;
@@ -1182,7 +1435,13 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, st
     *why = "n and k must be multiples of 8 (16-byte rows)";
     return AXON_EINVAL;
   }
-  if (!tile_ok(tm, tn)) {
+  if (qkv_wide && !qkv_wide_tile_ok(tm, tn)) {
+    *why = "hw variant 3 tiles: TILES_IN_BLOCK_M 1 or 2 (64 or 128 rows), TILES_IN_BLOCK_N 1 or 2 "
+           "(256 or 512 columns, one wave per 64)";
+    return AXON_EINVAL;
+  }
+  if (qkv_wide) tn *= kQkvWideCols / 64;  // in 64-column units from here on
+  if (!qkv_wide && !tile_ok(tm, tn)) {
     *why = "TILES_IN_BLOCK_M/N must each be 1, 2 or 4 (tiles of 64, 128 or 256)";
     return AXON_EINVAL;
   }
@@ -1198,7 +1457,8 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int tm, int tn, int tk, st
   }
   const Plan p = plan_of(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), tm, tn, tk);
   if (!grid_fits(static_cast<int64_t>(p.S) * p.MT * p.NT, 1, threads) ||
-      (p.S > 1 && !grid_fits((M * N / 4 + 255) / 256, 1, 256))) {
+      (p.S > 1 && !grid_fits((M * N / 4 + 255) / 256, 1, 256)) ||
+      (qkv_wide && !grid_fits((K + 63) / 64, static_cast<int64_t>(p.NT) * p.BN / kPackCols, 256))) {
     *why = "grid too large for one dispatch (fewer than 2^32 work-items)";
     return AXON_EINVAL;
   }
@@ -1403,6 +1663,42 @@ int dispatch_qkv(int BM, int BN, const GemmArgs& g, hipStream_t st) {
   AXON_GEMM_CASE(256, 256)
 #undef AXON_GEMM_CASE
   set_error("no GEMM instantiation for this tile");
+  return AXON_EINVAL;
+}
+
+// qkv_cte hw variant 3: pack w, then the full-width GEMM, then (split K) the
+// fixup. Every grid is checked before the first launch.
+template <int BM, int NW>
+void launch_qkv_wide(const GemmArgs& g, const u32x4* wp, int nct, hipStream_t st) {
+  const unsigned blocks = static_cast<unsigned>(g.S * g.MT * g.NT);
+  hipLaunchKernelGGL((qkv_wide_kernel<BM, NW>), dim3(blocks), dim3(64 * NW), 0, st, g, wp, nct);
+  if (g.S > 1) {
+    const int64_t quads = static_cast<int64_t>(g.M) * g.N / 4;
+    hipLaunchKernelGGL(splitk_reduce_kernel<kQkv>, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
+                       st, g, 64 * NW);
+  }
+}
+
+int dispatch_qkv_wide(int BM, int BN, const GemmArgs& g, const bf16* w, u32x4* wp, int kp64, int np, int nct,
+                      hipStream_t st) {
+  if (const int rc = gemm_grid_check(g, BN); rc != AXON_OK) return rc;
+  if (const int rc = grid_check("qkv_pack_w_kernel", kp64 / 64, np / kPackCols, 256); rc != AXON_OK) return rc;
+  if (kp64 > 0) {
+    hipLaunchKernelGGL(qkv_pack_w_kernel, dim3(static_cast<unsigned>(kp64 / 64), static_cast<unsigned>(np / kPackCols)),
+                       dim3(256), 0, st, w, wp, g.K, g.N, nct);
+    if (const int rc = launch_status("qkv_pack_w_kernel"); rc != AXON_OK) return rc;
+  }
+#define AXON_QKV_WIDE_CASE(bm, bn)                                          \
+  if (BM == bm && BN == bn) {                                               \
+    launch_qkv_wide<bm, bn / 64>(g, wp, nct, st);                           \
+    return launch_status("qkv_wide_kernel");                                \
+  }
+  AXON_QKV_WIDE_CASE(64, 256)
+  AXON_QKV_WIDE_CASE(64, 512)
+  AXON_QKV_WIDE_CASE(128, 256)
+  AXON_QKV_WIDE_CASE(128, 512)
+#undef AXON_QKV_WIDE_CASE
+  set_error("no qkv_cte hw variant 3 instantiation for this tile");
   return AXON_EINVAL;
 }
 
@@ -1830,7 +2126,10 @@ const char* summary_mlp(int) {
 // that hw variant runs over K' = k (bf16) or 3k (fp32 hi|lo|hi planes).
 // hw variant 2 (bf16 only): no prep pass; the GEMM's A loads read the three
 // residual inputs and sum them (kQkv), K' = k.
+// hw variant 3 (bf16 only): as 2, over full-width N tiles with w packed into
+// MFMA operand order by a pre-pass (qkv_wide_kernel).
 constexpr int kQkvFused = 2;
+constexpr int kQkvWide = 3;
 
 int qkv_kp(int64_t k, int dtype) { return static_cast<int>(dtype == AXON_F32 ? 3 * k : k); }
 
@@ -1849,22 +2148,43 @@ int check_qkv(const Call& c, std::string* why) {
       *why = "all four inputs must share one dtype";
       return AXON_EDTYPE;
     }
-  if (c.variant == kQkvFused && dt != AXON_BF16) {
-    *why = "hw variant 2 sums bf16 residual inputs inside the GEMM; fp32 inputs use hw variants 0 and 1";
+  if ((c.variant == kQkvFused || c.variant == kQkvWide) && dt != AXON_BF16) {
+    *why = "hw variants 2 and 3 sum bf16 residual inputs inside the GEMM; fp32 inputs use hw variants 0 and 1";
     return AXON_EDTYPE;
   }
   if (c.dim(2) > (1 << 28)) {
     *why = "k out of range";
     return AXON_EINVAL;
   }
+  if (c.variant == kQkvWide)
+    return check_gemm_shape(c.dim(0), c.dim(1), c.dim(2), c.tile(0), c.tile(1), c.tile(2), why,
+                            kQkvWideCols * c.tile(1), true);
   return check_gemm_shape(c.dim(0), c.dim(1), qkv_kp(c.dim(2), dt), c.tile(0), c.tile(1), c.tile(2), why);
 }
 
 int manifest_qkv(int v, const int64_t* dims, int dt, Constraint* out, int cap) {
   const int64_t mnk[3] = {dims[0], dims[1], dt == AXON_F32 ? 3 * dims[2] : dims[2]};
-  const int n = manifest_splitk(v, mnk, dt, out, cap);
-  // The fused variant has no fp32 instantiation: an extent of 0 admits no tile.
-  if (v == kQkvFused && dt != AXON_BF16)
+  int n = 0;
+  if (v == kQkvWide) {
+    if (cap < 3) return 0;
+    // Tiles of 64 or 128 rows and 256 or 512 columns (N counted in units of
+    // 256); K range capped where the grid of the largest tile stops reaching
+    // kMinGroups workgroups.
+    const int64_t m = std::max<int64_t>(dims[0], 1), nn = std::max<int64_t>(dims[1], 1);
+    const int64_t bm = m >= 128 ? 128 : 64, bn = nn > 256 ? 512 : 256;
+    const int64_t tiles = cdiv64(m, bm) * cdiv64(nn, bn), K = std::max<int64_t>(dims[2], 1);
+    const int64_t kext = k_extent(dims[2]);
+    int64_t range = kKUnit;
+    while (range * 2 <= kext && tiles * cdiv64(K, range * 2) >= kMinGroups) range *= 2;
+    out[0] = {"TILES_IN_BLOCK_M", bm, 64, false};
+    out[1] = {"TILES_IN_BLOCK_N", bn, kQkvWideCols, false};
+    out[2] = {"TILES_IN_BLOCK_K", range, kKUnit, false};
+    n = 3;
+  } else {
+    n = manifest_splitk(v, mnk, dt, out, cap);
+  }
+  // The fused variants have no fp32 instantiation: an extent of 0 admits no tile.
+  if ((v == kQkvFused || v == kQkvWide) && dt != AXON_BF16)
     for (int i = 0; i < n; ++i) out[i].extent = 0;
   return n;
 }
@@ -1877,16 +2197,26 @@ struct QkvLayout {
 };
 
 // qkv_cte workspace: [row scales fp32 m][A' bf16 m x K'][B' bf16 K' x n
-// (fp32 inputs only)][split-K data of the GEMM over K'].
+// (fp32 inputs only)][split-K data of the GEMM over K']. hw variant 2: the
+// split-K data only; hw variant 3: [packed w, Kp x Np bf16 (Kp = k rounded up
+// to 64, Np = N tiles x BN)][split-K data].
 QkvLayout qkv_layout(const Call& c) {
   const int m = static_cast<int>(c.dim(0)), n = static_cast<int>(c.dim(1));
   QkvLayout L;
   L.kp = qkv_kp(c.dim(2), c.dtype(0));
-  L.p = plan_of(m, n, L.kp, c.tile(0), c.tile(1), c.tile(2));
+  L.p = plan_of(m, n, L.kp, c.tile(0), c.variant == kQkvWide ? c.tile(1) * (kQkvWideCols / 64) : c.tile(1),
+                c.tile(2));
   L.scale = 0;
   if (c.variant == kQkvFused) {  // split-K data only
     L.a = L.b = L.data = 0;
     L.total = data_bytes(L.p, m, n, 1);
+    return L;
+  }
+  if (c.variant == kQkvWide) {
+    L.a = L.b = 0;
+    const size_t kp64 = (static_cast<size_t>(c.dim(2)) + 63) / 64 * 64;
+    L.data = align256(kp64 * static_cast<size_t>(L.p.NT) * L.p.BN * sizeof(bf16));
+    L.total = L.data + data_bytes(L.p, m, n, 1);
     return L;
   }
   L.a = align256(static_cast<size_t>(m) * sizeof(float));
@@ -1917,6 +2247,15 @@ int launch_qkv(const Call& c, const void* const* in, void* const* out, void* ws,
     return AXON_EARG;
   }
   const float eps = 1e-6f;
+  if (c.variant == kQkvWide) {
+    const int kp64 = (k + 63) / 64 * 64, np = L.p.NT * L.p.BN, nct = np / 32;
+    u32x4* wp = static_cast<u32x4*>(ws);
+    char* base = static_cast<char*>(ws);
+    GemmArgs g = make_args(in[0], nullptr, nullptr, out[0], m, n, k, L.p, base + L.data, 1, eps);
+    g.A2 = static_cast<const bf16*>(in[1]);
+    g.A3 = static_cast<const bf16*>(in[2]);
+    return dispatch_qkv_wide(L.p.BM, L.p.BN, g, static_cast<const bf16*>(in[3]), wp, kp64, np, nct, st);
+  }
   if (c.variant == kQkvFused) {
     GemmArgs g = make_args(in[0], static_cast<const bf16*>(in[3]), nullptr, out[0], m, n, k, L.p, ws, 1, eps);
     g.A2 = static_cast<const bf16*>(in[1]);
@@ -1957,6 +2296,12 @@ int launch_qkv(const Call& c, const void* const* in, void* const* out, void* ws,
 }
 
 const char* summary_qkv(int variant) {
+  if (variant == kQkvWide)
+    return "bf16 only: the fused residual sum of hw variant 2 over full-width N tiles (TILES_IN_BLOCK_M "
+           "x 64 rows by TILES_IN_BLOCK_N x 256 columns, one wave per 64 columns), so each residual row is "
+           "read once per K range; "
+           "A staged in LDS, w packed by a pre-pass into MFMA operand order and loaded straight into "
+           "registers (one contiguous KiB per wave load), split-K fixup applies the row scale";
   if (variant == kQkvFused)
     return "bf16 only: one GEMM whose A loads read x, mlp_prev and attention_prev and add them in "
            "fp32 (sum of squares taken on the fly, as rmsnorm_matmul_eps), so the residual sum never "
@@ -2379,7 +2724,7 @@ const Family* family_silu_mlp() {
 }
 
 const Family* family_qkv_cte() {
-  static const Family f = {"qkv_cte", 3, 4, 1, 3, kTileArgs3, 3, summary_qkv, manifest_qkv,
+  static const Family f = {"qkv_cte", 4, 4, 1, 3, kTileArgs3, 3, summary_qkv, manifest_qkv,
                            check_qkv, workspace_qkv, outputs_qkv, launch_qkv};
   return &f;
 }

@@ -49,7 +49,7 @@ KERNEL_OF = {
     "matmul_std002": "gemm_kernel",
     "rmsnorm_matmul_eps": "gemm_kernel",
     "attention_causal": "attn_",
-    "qkv_cte": "gemm_kernel",
+    "qkv_cte": "qkv_wide_kernel",
 }
 
 

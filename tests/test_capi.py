@@ -137,7 +137,8 @@ def test_legal_tiles_are_a_subset_of_the_manifest():
     [
         ("matmul_std002", [1024, 512, 16384], (2, 2, 8)),
         ("rmsnorm_matmul_eps", [1024, 512, 16384], (2, 2, 8)),
-        ("qkv_cte", [16384, 512, 8192], (4, 4, 16)),
+        # hw variant 3 counts N in units of 256 columns: its fastest is 128 x 512.
+        ("qkv_cte", [16384, 512, 8192], {0: (4, 4, 16), 1: (4, 4, 16), 2: (4, 4, 16), 3: (2, 2, 16)}),
     ],
 )
 def test_default_budget_benches_the_fastest_tuple(name, dims, best):
@@ -155,7 +156,8 @@ def test_default_budget_benches_the_fastest_tuple(name, dims, best):
         cons = hip.manifest(name, v, dims, hip.AXON_BF16)
         legal = [t for t in product(spec.tile_options, repeat=len(spec.tile_args))
                  if rejection_reason(spec.tile_args, t, cons) is None]
-        assert best in select_diverse(legal, budget=8, seed=SEED), (name, v, legal)
+        want = best[v] if isinstance(best, dict) else best
+        assert want in select_diverse(legal, budget=8, seed=SEED), (name, v, legal)
 
 
 def test_manifest_admits_only_legal_tiles():

@@ -7,7 +7,8 @@ fp32 cases to the reference's rtol = atol = 1e-3 (the split-precision GEMM
 keeps about 1e-5). Shapes: the reference's vision_l4 (ragged m = 578,
 n = 264) and llama405b_1k cases in both dtypes, over a diverse selection of
 legal tile tuples in every hw variant (split-K and single-pass schedules;
-hw variant 2, the fused residual sum, takes bf16 only),
+hw variants 2 and 3, the fused residual sum, take bf16 only; hw variant 3
+counts TILES_IN_BLOCK_N in units of 256 columns),
 plus small edge shapes (one row, k = 8, m = 0). The llama70b case
 (16384 x 512 x 8192) is checked against torch's fp32 product on the GPU."""
 
@@ -46,8 +47,9 @@ def test_qkv_edge_shapes(sizes, dtype):
     assert check_parity("qkv_cte", sizes, rtol=tol, atol=tol, dtype=dtype, budget=4, variants=variants)
 
 
-def test_qkv_fused_variant_refuses_fp32():
-    st, why = hip.check("qkv_cte", 2, (2, 2, 4), [256, 128, 4096], [hip.AXON_F32] * 4)
+@pytest.mark.parametrize("variant", [2, 3])
+def test_qkv_fused_variant_refuses_fp32(variant):
+    st, why = hip.check("qkv_cte", variant, (2, 2, 4), [256, 128, 4096], [hip.AXON_F32] * 4)
     assert st == hip.AXON_EDTYPE and "bf16" in why
 
 
@@ -63,7 +65,7 @@ def test_qkv_zero_rows_is_a_no_op():
     assert torch.all(out == 7.0)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_qkv_llama70b_against_torch_fp32(variant):
     """Full llama70b shape (16384 x 512 x 8192, bf16 inputs), split-K tiles:
     compared with torch's fp32 restatement of the reference formula on the
@@ -80,8 +82,8 @@ def test_qkv_llama70b_against_torch_fp32(variant):
     torch.testing.assert_close(ln.outputs[0].float(), ref, rtol=2e-2, atol=2e-2)
 
 
-@pytest.mark.parametrize(("dtype", "variant"), [(None, 1), (None, 2), ("float32", 1)],
-                         ids=["bf16-v1", "bf16-v2", "fp32-v1"])
+@pytest.mark.parametrize(("dtype", "variant"), [(None, 1), (None, 2), (None, 3), ("float32", 1)],
+                         ids=["bf16-v1", "bf16-v2", "bf16-v3", "fp32-v1"])
 def test_qkv_repeated_launches_bit_identical(dtype, variant):
     """Split-K sums its partials in a fixed order and the prep pass is
     elementwise, so relaunching over the same workspace reproduces the
@@ -102,16 +104,19 @@ def test_qkv_repeated_launches_bit_identical(dtype, variant):
 
 @pytest.mark.parametrize(("sizes", "dtype", "variant"),
                          [((16384, 640, 12288), torch.bfloat16, 2), ((16384, 640, 12288), torch.bfloat16, 1),
-                          ((8192, 512, 16384), torch.bfloat16, 2), ((8192, 512, 16384), torch.float32, 1),
+                          ((16384, 640, 12288), torch.bfloat16, 3),
+                          ((8192, 512, 16384), torch.bfloat16, 2), ((8192, 512, 16384), torch.bfloat16, 3),
+                          ((8192, 512, 16384), torch.float32, 1),
                           ((16384, 512, 8192), torch.float32, 0), ((16384, 640, 12288), torch.float32, 1)],
-                         ids=["mistral123b-v2", "mistral123b-v1", "llama405b_8k-v2", "llama405b_8k_fp32-v1",
-                              "llama70b_fp32-v0", "mistral123b_fp32-v1"])
+                         ids=["mistral123b-v2", "mistral123b-v1", "mistral123b-v3", "llama405b_8k-v2",
+                              "llama405b_8k-v3", "llama405b_8k_fp32-v1", "llama70b_fp32-v0", "mistral123b_fp32-v1"])
 def test_qkv_large_reference_cases(sizes, dtype, variant):
     """The reference's large cases (mistral123b, n = 640: a ragged last N tile
     at 128 or 256 columns; llama405b_8k; the fp32 llama70b / mistral123b /
     llama405b_8k) at full size, inputs drawn on the GPU, against torch's fp32
     restatement of the reference formula, at the reference's tolerances
-    (bf16: rtol 5e-2, atol 1.5e-1; fp32: 1e-3)."""
+    (bf16: rtol 5e-2, atol 1.5e-1; fp32: 1e-3). hw variant 3's (2, 2, 8) is a
+    128 x 512 tile: at n = 640 its second N tile holds 128 live columns."""
     m, n, k = sizes
     g = torch.Generator(device="cuda").manual_seed(5)
     x, mp, ap = (torch.randn(m, k, device="cuda", generator=g).to(dtype) for _ in range(3))
