@@ -695,27 +695,35 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) 
   // RMSNorm epilogues: the row scales of this block's rows (the block's
   // 1024 outputs span at most 1024 / N + 1 rows, N >= 8) are summed over
   // the splits once, by one thread per row, instead of by every thread.
+  // Their loads and the partial loads below are all issued before the first
+  // wait, so the two reads overlap; threads past the output load a clamped
+  // quad (MN % 8 == 0) and return after the barrier.
   __shared__ float row_scale[129];
+  float ss = 0.f;
+  bool own_row = false;
   if constexpr (RMS) {
     const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x * 4;
     const int r0 = static_cast<int>(first / g.N);
     const int r1 = static_cast<int>(min(first + static_cast<int64_t>(blockDim.x) * 4, MN) - 1) / g.N;
     const int r = r0 + static_cast<int>(threadIdx.x);
     if (r <= r1) {
-      const int nt = 0;  // every N tile holds the same row sums; read tile 0's
-      float ss = 0.f;
-      for (int zz = 0; zz < g.S; ++zz) ss += g.rowsq[(static_cast<int64_t>(zz) * g.NT + nt) * g.M + r];
-      row_scale[threadIdx.x] = EPI == kRmsSum    ? 1.f / sqrtf(ss)
-                               : EPI == kSoftmax ? 1.f / ss
-                                                 : 1.f / sqrtf(ss / static_cast<float>(g.K) + g.eps);
+      own_row = true;
+      // Every N tile holds the same row sums; read tile 0's, in split order.
+      const float* rq = g.rowsq + r;
+      const int64_t zs = static_cast<int64_t>(g.NT) * g.M;
+      int zz = 0;
+      for (; zz + 4 <= g.S; zz += 4) {
+        const float a0 = rq[(zz + 0) * zs], a1 = rq[(zz + 1) * zs], a2 = rq[(zz + 2) * zs], a3 = rq[(zz + 3) * zs];
+        ss = (((ss + a0) + a1) + a2) + a3;
+      }
+      for (; zz < g.S; ++zz) ss += rq[zz * zs];
     }
-    __syncthreads();
   }
-  if (idx >= MN) return;
+  const int64_t lidx = min(idx, MN - 4);
   float v[NB][4];
 #pragma unroll
   for (int q = 0; q < NB; ++q) {
-    const float* base = g.partial + static_cast<int64_t>(q) * g.S * MN + idx;
+    const float* base = g.partial + static_cast<int64_t>(q) * g.S * MN + lidx;
     float t[4] = {0.f, 0.f, 0.f, 0.f};
     int zz = 0;
     for (; zz + 4 <= g.S; zz += 4) {
@@ -734,6 +742,14 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int BN) 
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[q][e] = t[e];
   }
+  if constexpr (RMS) {
+    if (own_row)
+      row_scale[threadIdx.x] = EPI == kRmsSum    ? 1.f / sqrtf(ss)
+                               : EPI == kSoftmax ? 1.f / ss
+                                                 : 1.f / sqrtf(ss / static_cast<float>(g.K) + g.eps);
+    __syncthreads();
+  }
+  if (idx >= MN) return;
   float sc = 1.f;
   (void)BN;
   // Output block of a column-split C (a quad never straddles: ncol % 8 == 0).
