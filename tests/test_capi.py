@@ -319,6 +319,27 @@ def test_workspace_sizes():
     assert hip.workspace_bytes("matmul", 0, [2, 2, 8], [1024, 512, 16384], [0, 0]) > 8 * 1024 * 512 * 4
 
 
+def test_qkv_full_width_variant_tiles_and_workspace():
+    """qkv_cte hw variant 3 counts TILES_IN_BLOCK_N in units of 256 columns
+    (1 or 2) and rows in units of 64 (1 or 2), takes bf16 only, and needs the
+    packed w (k rounded up to 64 x N tiles x BN, bf16) ahead of the split-K
+    partials and row sums."""
+    m, n, k = 16384, 512, 8192
+    bf16 = [hip.AXON_BF16] * 4
+    assert hip.check("qkv_cte", 3, (2, 2, 16), [m, n, k], bf16)[0] == hip.AXON_OK
+    for tiles in [(2, 4, 16), (4, 2, 16), (2, 8, 16)]:
+        st, why = hip.check("qkv_cte", 3, tiles, [m, n, k], bf16)
+        assert st == hip.AXON_EINVAL and "TILES_IN_BLOCK_N 1 or 2" in why, (tiles, why)
+    assert hip.check("qkv_cte", 3, (2, 2, 16), [m, n, k], [hip.AXON_F32] * 4)[0] == hip.AXON_EDTYPE
+    splits = k // (16 * 256)
+    packed = k * 512 * 2
+    assert hip.workspace_bytes("qkv_cte", 3, (2, 2, 16), [m, n, k], bf16) == (
+        packed + splits * m * n * 4 + splits * 1 * m * 4)
+    # One K range: no split-K data, only the packed w (here 640 columns -> two
+    # 512-column tiles, k = 1000 -> 1024 packed rows).
+    assert hip.workspace_bytes("qkv_cte", 3, (2, 2, 4), [96, 640, 1000], bf16) == 1024 * 1024 * 2
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(hip, "_lib", None)
     monkeypatch.setattr(hip, "LIB_PATH", tmp_path / "absent.so")
