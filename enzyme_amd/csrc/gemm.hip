@@ -1150,9 +1150,12 @@ __global__ __launch_bounds__(256) void split_rows_hilo_kernel(const float* __res
 // One workgroup per BM x BN output tile and K range, BN = 64 x waves, so at
 // n = 512 one N tile covers every column and each residual row leaves memory
 // once per K range. hw variant 2's 256 x 256 tiles read every A row twice,
-// once per N tile. Replayed as loads only (A rows plus the B block, 8 waves),
-// the two patterns take 227 and 155 us at 16384 x 512 x 8192. Wave w owns the
-// output columns 64 w .. 64 w + 63 of the tile and all BM rows:
+// once per N tile. Replayed as loads only (A rows plus the B block, 8 waves,
+// plain loads), the two patterns take 173 and 161 us at 16384 x 512 x 8192,
+// and 154 us for the full-width one with non-temporal A loads, which the
+// 256-column pattern cannot use (its second N tile then misses L2: 228 us).
+// Wave w owns the output columns 64 w .. 64 w + 63 of the tile and all BM
+// rows:
 //   * A, h = (x + mlp_prev) + attention_prev (summed in fp32, squares summed
 //     for the row scale, rounded to bf16), is staged once per K step in LDS
 //     and read by every wave;

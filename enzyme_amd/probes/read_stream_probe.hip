@@ -16,6 +16,8 @@
 // of each array per K step (the N tiles of one M tile read the same rows on
 // one XCD, as the GEMM's XCD-aware unit numbering places them), with PD steps
 // of loads issued before the first is consumed. RB = 128 is a 64-deep K step.
+// A is read with non-temporal loads unless a case says otherwise (plain loads
+// let the N tiles of one row block share lines in L2).
 //
 // Build and run (repository root):
 //   hipcc --offload-arch=gfx950 -O3 -Xclang -target-feature -Xclang -packed-fp32-ops \
@@ -79,7 +81,7 @@ constexpr int kM = 16384, kK = 8192, kS = 2;
 // rows, 64 vectors), columns nt*BN..+BN-1 (NT * BN == 512), k in the
 // workgroup's K range; thread t loads vectors u = t + i * T, u -> k row
 // u / (BN / 8), vector u % (BN / 8).
-template <int BM, int RB, int T, int PD, int BN = 0>
+template <int BM, int RB, int T, int PD, int BN = 0, bool NTA = true>
 __global__ __launch_bounds__(T) void tile_stream(const u32x4* __restrict__ a, const u32x4* __restrict__ w,
                                                  u32x4* __restrict__ sink, int NT) {
   constexpr int VPR = RB / 16;             // vectors per row per step
@@ -121,7 +123,10 @@ __global__ __launch_bounds__(T) void tile_stream(const u32x4* __restrict__ a, co
       for (int q = 0; q < 3; ++q)
 #pragma unroll
         for (int i = 0; i < V; ++i)
-          t[p][q][i] = __builtin_nontemporal_load(a + q * n16 + off[i] + min(s + p, nsteps - 1) * VPR);
+        {
+          const u32x4* src = a + q * n16 + off[i] + min(s + p, nsteps - 1) * VPR;
+          t[p][q][i] = NTA ? __builtin_nontemporal_load(src) : *src;
+        }
 #pragma unroll
       for (int i = 0; i < VB; ++i) tb[p][i] = w[boff[i] + min(s + p, nsteps - 1) * (RB / 2) * 64];
     }
@@ -139,26 +144,26 @@ __global__ __launch_bounds__(T) void tile_stream(const u32x4* __restrict__ a, co
   if (acc.x == 0x12345678u && acc.y == 0x9abcdefu && acc.z == 0x3u) sink[blockIdx.x] = acc;
 }
 
-template <int BM, int RB, int T, int PD, int BN = 0>
+template <int BM, int RB, int T, int PD, int BN = 0, bool NTA = true>
 void tile_case(const u32x4* const bufs[2], const u32x4* w, u32x4* sink, int NT) {
   const int G = kS * (kM / BM) * NT;
   hipEvent_t a, b;
   CK(hipEventCreate(&a));
   CK(hipEventCreate(&b));
   for (int r = 0; r < 6; ++r)
-    hipLaunchKernelGGL((tile_stream<BM, RB, T, PD, BN>), dim3(G), dim3(T), 0, 0, bufs[r & 1], w, sink, NT);
+    hipLaunchKernelGGL((tile_stream<BM, RB, T, PD, BN, NTA>), dim3(G), dim3(T), 0, 0, bufs[r & 1], w, sink, NT);
   CK(hipGetLastError());
   CK(hipEventRecord(a));
   for (int r = 0; r < g_reps; ++r)
-    hipLaunchKernelGGL((tile_stream<BM, RB, T, PD, BN>), dim3(G), dim3(T), 0, 0, bufs[r & 1], w, sink, NT);
+    hipLaunchKernelGGL((tile_stream<BM, RB, T, PD, BN, NTA>), dim3(G), dim3(T), 0, 0, bufs[r & 1], w, sink, NT);
   CK(hipEventRecord(b));
   CK(hipEventSynchronize(b));
   float ms = 0.f;
   CK(hipEventElapsedTime(&ms, a, b));
   const double us = ms * 1e3 / g_reps;
   const double bytes = 3.0 * kM * kK * 2;
-  std::printf("tile  BM %3d  N tiles %d  BN %3d  G %4d  RB %3d  T %4d  PD %d: %8.2f us  %6.0f GB/s (unique A bytes)\n", BM, NT,
-              BN, G, RB, T, PD, us, bytes / (us * 1e-6) / 1e9);
+  std::printf("tile  BM %3d  N tiles %d  BN %3d  G %4d  RB %3d  T %4d  PD %d  A %s: %8.2f us  %6.0f GB/s (unique A bytes)\n",
+              BM, NT, BN, G, RB, T, PD, NTA ? "nt " : "reg", us, bytes / (us * 1e-6) / 1e9);
   CK(hipEventDestroy(a));
   CK(hipEventDestroy(b));
 }
@@ -248,6 +253,13 @@ int main(int argc, char** argv) {
   tile_case<128, 128, 512, 1, 512>(cb, w, sink, 1);
   tile_case<128, 128, 512, 2, 512>(cb, w, sink, 1);
   tile_case<128, 256, 256, 1, 512>(cb, w, sink, 1);
+  // Plain A loads: the N tiles of one row block can share lines in L2.
+  tile_case<256, 128, 256, 1, 0, false>(cb, w, sink, 2);
+  tile_case<256, 128, 512, 2, 0, false>(cb, w, sink, 2);
+  tile_case<128, 128, 256, 1, 0, false>(cb, w, sink, 1);
+  tile_case<256, 128, 256, 1, 256, false>(cb, w, sink, 2);
+  tile_case<256, 128, 512, 1, 256, false>(cb, w, sink, 2);
+  tile_case<128, 128, 512, 1, 512, false>(cb, w, sink, 1);
   for (auto& p : bufs) CK(hipFree(p));
   CK(hipFree(w));
   CK(hipFree(sink));
