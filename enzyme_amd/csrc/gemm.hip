@@ -40,9 +40,15 @@
 // gfx950's transposing LDS read (ds_read_b64_tr_b16): two reads give a lane
 // the 8 consecutive k values of its column.
 //
+// qkv_cte hw variant 3 (qkv_wide_kernel, with its own comment below) is a
+// separate schedule: full-width N tiles of 256 or 512 columns, one wave per
+// 64 columns, w packed into MFMA operand order by qkv_pack_w_kernel and
+// loaded straight into registers.
+//
 // Tile arguments: TILES_IN_BLOCK_M = BM/64, TILES_IN_BLOCK_N = BN/64 (tiles of
-//                 64, 128 or 256), TILES_IN_BLOCK_K = K range per workgroup /
-//                 256 (silu_mlp: TILES_IN_BLOCK_P = BN/64 of its second GEMM).
+//                 64, 128 or 256; qkv_cte hw variant 3: BN/256), TILES_IN_BLOCK_K
+//                 = K range per workgroup / 256 (silu_mlp: TILES_IN_BLOCK_P =
+//                 BN/64 of its second GEMM).
 // Every tuple the manifest admits is instantiated: silu_mlp narrows its
 // stages' tiles to what its two accumulator sets and LDS hold (BM x BN <=
 // 128 x 128 per stage, BM <= 128 in stage 2) instead of refusing them.
